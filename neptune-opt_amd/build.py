@@ -1,0 +1,57 @@
+"""Build step of the neptune HIP backend (no GPU needed).
+
+1. hipcc builds the C-ABI runtime libneptune_hip.so (host code: hiprtc + module launch) in
+   place, next to the Python package, so that it travels with the source tree.
+2. Every generated kernel unit the benchmark configurations and tests use is compiled with
+   hiprtc for gfx950 into the on-disk code-object cache (neptune_codegen/_codeobj).  That both
+   proves each emitted unit compiles and spares the GPU host the compile.
+"""
+from __future__ import annotations
+
+import os
+import pathlib
+import subprocess
+import sys
+
+ROOT = pathlib.Path(__file__).resolve().parent
+REPO = ROOT.parent
+LIB = ROOT / "neptune_codegen" / "_lib" / "libneptune_hip.so"
+SRC = ROOT / "csrc" / "nep_runtime.cpp"
+
+
+def build_library(verbose: bool = True) -> pathlib.Path:
+    LIB.parent.mkdir(parents=True, exist_ok=True)
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc, "--offload-arch=gfx950", "-O2", "-fPIC", "-shared", "-std=c++17",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           f"-I{REPO / 'include'}", str(SRC), "-o", str(tmp),
+           "-L/opt/rocm/lib", "-lhiprtc", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"]
+    if verbose:
+        print("[build]", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def precompile(verbose: bool = True) -> int:
+    """hiprtc-compile the kernel units of the benchmark and test shapes into the cache."""
+    sys.path.insert(0, str(ROOT))
+    import neptune_codegen as CG
+
+    count = 0
+    for program in CG.prebuilt_programs():
+        size = program.precompile()
+        count += 1
+        if verbose:
+            print(f"[build] {program.name}: {size} bytes", flush=True)
+    return count
+
+
+def main() -> None:
+    build_library()
+    precompile()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,534 @@
+// nep_fold.h -- row folds for scalar repair skeletons on gfx950.
+//
+// A fold reduces every row of a [rows, ncols] strided matrix to one value through the state
+// (m, acc, seen, status): m is the producer value (a running max or sum), acc the consumer
+// accumulator kept in the coordinate of m, seen whether any element was folded, status the
+// NaN (bit 0) / +inf (bit 1) flags of exponential folds.  Semantics follow the reference's
+// generated chunk / merge_state / finalize helpers (neptune_codegen/emitters.py:436-532); the
+// algebra of one skeleton arrives as a policy struct F written by the HIP emitter:
+//
+//   static constexpr bool kLog, kProducerSum, kConsumerMax, kFloor, kHasBias;
+//   static float phi(float v, float n)              producer operand of one element
+//   static float term(float v, float den, float n)  consumer term at producer value den
+//   static float rho(float q, float q2)             repair slope from coordinate q to q2
+//   static float beta(float q, float q2)            repair bias (max consumers only)
+//   static float finalize(float m, float acc, float n)
+//
+// Mapping (MI355X): TPR lanes cooperate on one row (TPR <= 64: several rows per wavefront;
+// TPR > 64: several wavefronts per row, merged through LDS).  A row is walked in tiles of
+// TPR*UNROLL*VEC elements; lane t of the row owns slot (u, t) = elements
+// [tile + (u*TPR + t)*VEC, +VEC), so one wavefront-wide load instruction reads consecutive
+// 16-byte segments.  VECTOR=false is the general strided path (one element per slot).
+#pragma once
+
+namespace nep {
+
+struct State {
+  float m;
+  float acc;
+  int seen;
+  int status;
+};
+
+template <class F>
+__device__ __forceinline__ float eff(float m) {
+  if constexpr (F::kFloor) return __builtin_fmaxf(m, 1e-30f);
+  else return m;
+}
+
+template <class F>
+__device__ __forceinline__ float consumer_init() {
+  return F::kConsumerMax ? -kInf : 0.0f;
+}
+
+// The reference's associative merge (emitters.py:491-517): sanitise both sides before the
+// repair is evaluated, transport each accumulator to the combined coordinate, keep the
+// non-empty side when only one is seen.  Commutative bit for bit, so butterfly partners agree.
+template <class F>
+__device__ __forceinline__ State merge_state(const State& A, const State& B) {
+  const bool vA = A.seen != 0, vB = B.seen != 0, both = vA && vB;
+  const float cm = F::kProducerSum ? (A.m + B.m) : __builtin_fmaxf(A.m, B.m);
+  const float oldA = both ? A.m : 1.0f, oldB = both ? B.m : 1.0f, fresh = both ? cm : 1.0f;
+  const float qA = eff<F>(oldA), qB = eff<F>(oldB), qN = eff<F>(fresh);
+  const float sA = both ? A.acc : 0.0f, sB = both ? B.acc : 0.0f;
+  float tA = sA * F::rho(qA, qN), tB = sB * F::rho(qB, qN);
+  if constexpr (F::kHasBias) {
+    tA += F::beta(qA, qN);
+    tB += F::beta(qB, qN);
+  }
+  const float ca = F::kConsumerMax ? __builtin_fmaxf(tA, tB) : (tA + tB);
+  State R;
+  R.m = vA ? (vB ? cm : A.m) : B.m;
+  R.acc = vA ? (vB ? ca : A.acc) : B.acc;
+  R.seen = (vA || vB) ? 1 : 0;
+  R.status = A.status | B.status;
+  return R;
+}
+
+template <int S>
+__device__ __forceinline__ State partner_state(const State& s) {
+  State o;
+  o.m = partner<S>(s.m);
+  o.acc = partner<S>(s.acc);
+  o.seen = partner<S>(s.seen);
+  o.status = partner<S>(s.status);
+  return o;
+}
+
+template <class F, int G>
+__device__ __forceinline__ State group_merge(State s) {
+  if constexpr (G >= 2) s = merge_state<F>(s, partner_state<1>(s));
+  if constexpr (G >= 4) s = merge_state<F>(s, partner_state<2>(s));
+  if constexpr (G >= 8) s = merge_state<F>(s, partner_state<4>(s));
+  if constexpr (G >= 16) s = merge_state<F>(s, partner_state<8>(s));
+  if constexpr (G >= 32) s = merge_state<F>(s, partner_state<16>(s));
+  if constexpr (G >= 64) s = merge_state<F>(s, partner_state<32>(s));
+  return s;
+}
+
+// Fast exponential-fold lane state: m = max finite phi so far (-inf when none), acc the sum of
+// exp(phi - m).  NaN or +inf inputs poison acc (exp(NaN) / exp(inf - inf)); a NaN in a tile with
+// no finite element sets `flag`.  Either marks the row for the exact path.
+struct LogLane {
+  float m;
+  float acc;
+  int flag;
+};
+
+__device__ __forceinline__ LogLane log_merge(const LogLane& A, const LogLane& B) {
+  LogLane R;
+  R.m = __builtin_fmaxf(A.m, B.m);
+  const float a = A.acc * fast_exp(A.m - R.m) + B.acc * fast_exp(B.m - R.m);
+  R.acc = (R.m == -kInf) ? 0.0f : a;
+  R.flag = A.flag | B.flag;
+  return R;
+}
+
+template <int G>
+__device__ __forceinline__ LogLane log_group_merge(LogLane s) {
+#define NEP_LOG_STEP(S)                                                   \
+  {                                                                       \
+    LogLane o;                                                            \
+    o.m = partner<S>(s.m);                                                \
+    o.acc = partner<S>(s.acc);                                            \
+    o.flag = partner<S>(s.flag);                                          \
+    s = log_merge(s, o);                                                  \
+  }
+  if constexpr (G >= 2) NEP_LOG_STEP(1)
+  if constexpr (G >= 4) NEP_LOG_STEP(2)
+  if constexpr (G >= 8) NEP_LOG_STEP(4)
+  if constexpr (G >= 16) NEP_LOG_STEP(8)
+  if constexpr (G >= 32) NEP_LOG_STEP(16)
+  if constexpr (G >= 64) NEP_LOG_STEP(32)
+#undef NEP_LOG_STEP
+  return s;
+}
+
+// ---------------------------------------------------------------- tile access
+template <class St, int TPR, int UNROLL, bool VECTOR>
+struct Tiles {
+  typedef typename St::T T;
+  static constexpr int VEC = VECTOR ? St::kVec : 1;
+  static constexpr int K = UNROLL * VEC;
+  static constexpr int TILE = TPR * K;
+
+  // Load slot u of the tile starting at column `tile` into v[u*VEC ..]; returns whether the
+  // slot lies inside [.., c1).  Out-of-range slots issue no load.
+  __device__ static __forceinline__ bool load_slot(const T* row, i64 stride_col, i64 tile,
+                                                   i64 c1, int t, int u, float* v) {
+    const i64 e = tile + (i64)(u * TPR + t) * VEC;
+    if (e >= c1) return false;
+    if constexpr (VECTOR) {
+      St::unpack(load16(row + e), v + u * VEC);
+    } else {
+      v[u] = St::load(row + e * stride_col);
+    }
+    return true;
+  }
+};
+
+// ---------------------------------------------------------------- row-level combine
+// Rows of TPR lanes: TPR <= 64 combines with in-wavefront butterflies; TPR > 64 additionally
+// merges the row's wavefront results through LDS (WPR wavefronts per row).
+template <int TPR>
+struct RowComm {
+  static constexpr int G = TPR < 64 ? TPR : 64;
+  static constexpr int WPR = TPR > 64 ? TPR / 64 : 1;
+};
+
+// ---------------------------------------------------------------- exact path
+// The reference chunk (emitters.py:459-488) over one thread's slots of one tile, merged into
+// the running state.  Used by every non-exponential fold and, for exponential folds, only on
+// rows whose fast path met NaN or +inf.
+template <class F, class St, int TPR, int UNROLL, bool VECTOR>
+__device__ __forceinline__ void exact_tile(State& s, const typename St::T* row, i64 stride_col,
+                                           i64 tile, i64 c1, int t, float n) {
+  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+  float v[TL::K];
+  bool ok[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) ok[u] = TL::load_slot(row, stride_col, tile, c1, t, u, v);
+  State c;
+  if constexpr (F::kLog) {
+    int status = 0, seen = 0;
+    float m = -kInf;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (!ok[u]) continue;
+#pragma unroll
+      for (int j = 0; j < TL::VEC; ++j) {
+        const float p = F::phi(v[u * TL::VEC + j], n);
+        if (is_nan(p)) status |= 1;
+        if (p == kInf) status |= 2;
+        if (is_finite(p)) {
+          seen = 1;
+          m = __builtin_fmaxf(m, p);
+        }
+      }
+    }
+    const float den = seen ? m : 0.0f;
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (!ok[u]) continue;
+#pragma unroll
+      for (int j = 0; j < TL::VEC; ++j) {
+        const float p = F::phi(v[u * TL::VEC + j], n);
+        if (is_finite(p)) acc += fast_exp(p - den);
+      }
+    }
+    c.m = m;
+    c.acc = acc;
+    c.seen = seen;
+    c.status = status;
+  } else {
+    bool any = false;
+    float m = F::kProducerSum ? 0.0f : -kInf;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (!ok[u]) continue;
+      any = true;
+#pragma unroll
+      for (int j = 0; j < TL::VEC; ++j) {
+        const float o = F::phi(v[u * TL::VEC + j], n);
+        m = F::kProducerSum ? (m + o) : __builtin_fmaxf(m, o);
+      }
+    }
+    m = any ? m : 0.0f;
+    const float den = eff<F>(m);
+    float acc = consumer_init<F>();
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (!ok[u]) continue;
+#pragma unroll
+      for (int j = 0; j < TL::VEC; ++j) {
+        const float tv = F::term(v[u * TL::VEC + j], den, n);
+        acc = F::kConsumerMax ? __builtin_fmaxf(acc, tv) : (acc + tv);
+      }
+    }
+    c.m = m;
+    c.acc = acc;
+    c.seen = any ? 1 : 0;
+    c.status = 0;
+  }
+  s = merge_state<F>(s, c);
+}
+
+// Exact state of the columns [c0, c1) of one row, complete in every lane of the row.
+template <class F, class St, int TPR, int UNROLL, bool VECTOR>
+__device__ __forceinline__ State exact_row_state(const typename St::T* row, i64 stride_col,
+                                                 i64 c0, i64 c1, int t, float n,
+                                                 State* lds_state) {
+  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+  typedef RowComm<TPR> RC;
+  State s;
+  s.m = 0.0f;
+  s.acc = consumer_init<F>();
+  s.seen = 0;
+  s.status = 0;
+  for (i64 tile = c0; tile < c1; tile += TL::TILE)
+    exact_tile<F, St, TPR, UNROLL, VECTOR>(s, row, stride_col, tile, c1, t, n);
+  s = group_merge<F, RC::G>(s);
+  if constexpr (RC::WPR > 1) {
+    const int wave = threadIdx.x >> 6, first = (wave / RC::WPR) * RC::WPR;
+    __syncthreads();
+    if (lane_id() == 0) lds_state[wave] = s;
+    __syncthreads();
+    State r = lds_state[first];
+#pragma unroll
+    for (int w = 1; w < RC::WPR; ++w) r = merge_state<F>(r, lds_state[first + w]);
+    s = r;
+  }
+  return s;
+}
+
+// Final value of a row from its exact state (emitters.py:522-532 for exponential folds).
+template <class F>
+__device__ __forceinline__ float finalize_state(const State& s, float n) {
+  if constexpr (F::kLog) {
+    if (s.status & 1) return __builtin_nanf("");
+    if (s.status & 2) return kInf;
+    if (!s.seen) return -kInf;
+    return F::finalize(s.m, s.acc, n);
+  } else {
+    return F::finalize(s.m, s.acc, n);
+  }
+}
+
+// ---------------------------------------------------------------- fast exponential path
+template <class F, class St, int TPR, int UNROLL, bool VECTOR>
+__device__ __forceinline__ LogLane log_row_lane(const typename St::T* row, i64 stride_col,
+                                                i64 c0, i64 c1, int t, float n) {
+  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+  LogLane s;
+  s.m = -kInf;
+  s.acc = 0.0f;
+  s.flag = 0;
+  for (i64 tile = c0; tile < c1; tile += TL::TILE) {
+    float v[TL::K];
+    bool ok[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) ok[u] = TL::load_slot(row, stride_col, tile, c1, t, u, v);
+    float p[TL::K];
+    float tm = -kInf;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+#pragma unroll
+      for (int j = 0; j < TL::VEC; ++j) {
+        const int k = u * TL::VEC + j;
+        p[k] = ok[u] ? F::phi(v[k], n) : -kInf;
+        tm = __builtin_fmaxf(tm, p[k]);
+      }
+    }
+    const float mn = __builtin_fmaxf(s.m, tm);
+    if (mn == -kInf) {
+      // No finite or +inf value yet; a NaN would otherwise be skipped by the max.
+#pragma unroll
+      for (int k = 0; k < TL::K; ++k) s.flag |= is_nan(p[k]) ? 1 : 0;
+    } else {
+      float a = s.acc * fast_exp(s.m - mn);
+#pragma unroll
+      for (int k = 0; k < TL::K; ++k) a += fast_exp(p[k] - mn);
+      s.acc = a;
+      s.m = mn;
+    }
+  }
+  return s;
+}
+
+template <class F, int TPR>
+__device__ __forceinline__ LogLane log_row_combine(LogLane s, LogLane* lds) {
+  typedef RowComm<TPR> RC;
+  s = log_group_merge<RC::G>(s);
+  if constexpr (RC::WPR > 1) {
+    const int wave = threadIdx.x >> 6, first = (wave / RC::WPR) * RC::WPR;
+    if (lane_id() == 0) lds[wave] = s;
+    __syncthreads();
+    LogLane r = lds[first];
+#pragma unroll
+    for (int w = 1; w < RC::WPR; ++w) r = log_merge(r, lds[first + w]);
+    s = r;
+  }
+  return s;
+}
+
+// ---------------------------------------------------------------- kernel bodies
+// Serial plan: one output per row (template.py:41-54).  WG threads per workgroup, WG/TPR rows
+// per workgroup (one row when TPR >= WG).
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, int WG>
+__device__ __forceinline__ void fold_serial(const typename St::T* __restrict__ x,
+                                            typename St::T* __restrict__ out, i64 rows,
+                                            i64 ncols, i64 stride_row, i64 stride_col) {
+  static_assert(WG % 64 == 0 && (TPR <= 64 || WG % TPR == 0), "bad row mapping");
+  constexpr int RPW = WG / TPR;  // rows per workgroup
+  __shared__ State lds_state[WG / 64];
+  __shared__ LogLane lds_lane[WG / 64];
+  const int t = threadIdx.x % TPR;
+  const i64 row = (i64)blockIdx.x * RPW + threadIdx.x / TPR;
+  const bool live = row < rows;
+  const typename St::T* rp = x + (live ? row : 0) * stride_row;
+  const i64 c1 = live ? ncols : 0;
+  const float n = (float)ncols;
+  float result;
+  if constexpr (F::kLog) {
+    LogLane s = log_row_lane<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, 0, c1, t, n);
+    s = log_row_combine<F, TPR>(s, lds_lane);
+    const bool bad = s.flag != 0 || is_nan(s.acc);
+    // Rows with NaN/+inf take the exact reference path; `bad` is uniform across the row.
+    bool any_bad = bad;
+    if constexpr (TPR > 64) {
+      any_bad = __syncthreads_or(bad ? 1 : 0) != 0;
+    } else {
+      any_bad = __builtin_amdgcn_ballot_w64(bad) != 0;
+    }
+    if (any_bad) {
+      const State e = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, 0,
+                                                                   bad ? c1 : 0, t, n,
+                                                                   lds_state);
+      if (bad) result = finalize_state<F>(e, n);
+    }
+    if (!bad) result = (s.m == -kInf) ? -kInf : F::finalize(s.m, s.acc, n);
+  } else {
+    const State e = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, 0, c1, t, n,
+                                                                 lds_state);
+    result = finalize_state<F>(e, n);
+  }
+  if (live && t == 0) St::store(out + row, result);
+}
+
+// Split plan, partial kernel (template.py:137-148): virtual row vr = row*nparts + part covers
+// columns [part*block, min(ncols, (part+1)*block)) and writes its exact chunk state.
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, int WG>
+__device__ __forceinline__ void fold_split_partial(const typename St::T* __restrict__ x,
+                                                   float* __restrict__ pm,
+                                                   float* __restrict__ pa,
+                                                   int* __restrict__ pv,
+                                                   int* __restrict__ ps, i64 rows, i64 ncols,
+                                                   i64 stride_row, i64 stride_col,
+                                                   i64 nparts, i64 block) {
+  constexpr int RPW = WG / TPR;
+  __shared__ State lds_state[WG / 64];
+  __shared__ LogLane lds_lane[WG / 64];
+  const int t = threadIdx.x % TPR;
+  const i64 vr = (i64)blockIdx.x * RPW + threadIdx.x / TPR;
+  const bool live = vr < rows * nparts;
+  const i64 row = live ? vr / nparts : 0;
+  const i64 part = live ? vr % nparts : 0;
+  const typename St::T* rp = x + row * stride_row;
+  const i64 c0 = part * block;
+  i64 c1 = c0 + block;
+  c1 = c1 < ncols ? c1 : ncols;
+  if (!live) c1 = c0;
+  const float n = (float)ncols;
+  State out_state;
+  if constexpr (F::kLog) {
+    LogLane s = log_row_lane<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c0, c1, t, n);
+    s = log_row_combine<F, TPR>(s, lds_lane);
+    const bool bad = s.flag != 0 || is_nan(s.acc);
+    bool any_bad;
+    if constexpr (TPR > 64) any_bad = __syncthreads_or(bad ? 1 : 0) != 0;
+    else any_bad = __builtin_amdgcn_ballot_w64(bad) != 0;
+    out_state.m = s.m;
+    out_state.acc = s.acc;
+    out_state.seen = (s.m != -kInf) ? 1 : 0;
+    out_state.status = 0;
+    if (any_bad) {
+      const State e = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c0,
+                                                                   bad ? c1 : c0, t, n,
+                                                                   lds_state);
+      if (bad) out_state = e;
+    }
+  } else {
+    out_state = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c0, c1, t, n,
+                                                             lds_state);
+  }
+  if (live && t == 0) {
+    pm[vr] = out_state.m;
+    pa[vr] = out_state.acc;
+    pv[vr] = out_state.seen;
+    ps[vr] = out_state.status;
+  }
+}
+
+// Split plan, merge kernel (template.py:151-164): one wavefront per row folds the row's
+// nparts partial states with merge_state and finalizes.
+template <class F, class St>
+__device__ __forceinline__ void fold_split_merge(const float* __restrict__ pm,
+                                                 const float* __restrict__ pa,
+                                                 const int* __restrict__ pv,
+                                                 const int* __restrict__ ps,
+                                                 typename St::T* __restrict__ out, i64 rows,
+                                                 i64 ncols, i64 nparts) {
+  const int lane = threadIdx.x & 63;
+  const i64 row = (i64)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const bool live = row < rows;
+  State s;
+  s.m = 0.0f;
+  s.acc = consumer_init<F>();
+  s.seen = 0;
+  s.status = 0;
+  if (live) {
+    for (i64 p = lane; p < nparts; p += 64) {
+      const i64 slot = row * nparts + p;
+      State c;
+      c.m = pm[slot];
+      c.acc = pa[slot];
+      c.seen = pv[slot];
+      c.status = ps[slot];
+      s = merge_state<F>(s, c);
+    }
+  }
+  s = group_merge<F, 64>(s);
+  if (live && lane == 0) St::store(out + row, finalize_state<F>(s, (float)ncols));
+}
+
+// Two-pass plan (template.py:62-103): pass 1 reduces the producer over the row, pass 2 the
+// term with the producer held constant.  The second pass re-reads the row.
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, int WG>
+__device__ __forceinline__ void fold_two_pass(const typename St::T* __restrict__ x,
+                                              typename St::T* __restrict__ out, i64 rows,
+                                              i64 ncols, i64 stride_row, i64 stride_col) {
+  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+  typedef RowComm<TPR> RC;
+  constexpr int RPW = WG / TPR;
+  __shared__ float lds[WG / 64];
+  const int t = threadIdx.x % TPR;
+  const i64 row = (i64)blockIdx.x * RPW + threadIdx.x / TPR;
+  const bool live = row < rows;
+  const typename St::T* rp = x + (live ? row : 0) * stride_row;
+  const i64 c1 = live ? ncols : 0;
+  const float n = (float)ncols;
+  const int wave = threadIdx.x >> 6, first = (wave / RC::WPR) * RC::WPR;
+  // pass 1: the producer
+  float m = F::kProducerSum ? 0.0f : -kInf;
+  for (i64 tile = 0; tile < c1; tile += TL::TILE) {
+    float v[TL::K];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (!TL::load_slot(rp, stride_col, tile, c1, t, u, v)) continue;
+#pragma unroll
+      for (int j = 0; j < TL::VEC; ++j) {
+        const float o = F::phi(v[u * TL::VEC + j], n);
+        m = F::kProducerSum ? (m + o) : __builtin_fmaxf(m, o);
+      }
+    }
+  }
+  m = F::kProducerSum ? group_sum<RC::G>(m) : group_max<RC::G>(m);
+  if constexpr (RC::WPR > 1) {
+    if (lane_id() == 0) lds[wave] = m;
+    __syncthreads();
+    float r = lds[first];
+#pragma unroll
+    for (int w = 1; w < RC::WPR; ++w)
+      r = F::kProducerSum ? (r + lds[first + w]) : __builtin_fmaxf(r, lds[first + w]);
+    m = r;
+    __syncthreads();
+  }
+  // pass 2: the term at the final producer value
+  float acc = consumer_init<F>();
+  for (i64 tile = 0; tile < c1; tile += TL::TILE) {
+    float v[TL::K];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (!TL::load_slot(rp, stride_col, tile, c1, t, u, v)) continue;
+#pragma unroll
+      for (int j = 0; j < TL::VEC; ++j) {
+        const float tv = F::term(v[u * TL::VEC + j], m, n);
+        acc = F::kConsumerMax ? __builtin_fmaxf(acc, tv) : (acc + tv);
+      }
+    }
+  }
+  acc = F::kConsumerMax ? group_max<RC::G>(acc) : group_sum<RC::G>(acc);
+  if constexpr (RC::WPR > 1) {
+    if (lane_id() == 0) lds[wave] = acc;
+    __syncthreads();
+    float r = lds[first];
+#pragma unroll
+    for (int w = 1; w < RC::WPR; ++w)
+      r = F::kConsumerMax ? __builtin_fmaxf(r, lds[first + w]) : (r + lds[first + w]);
+    acc = r;
+  }
+  if (live && t == 0) St::store(out + row, F::finalize(m, acc, n));
+}
+
+}  // namespace nep

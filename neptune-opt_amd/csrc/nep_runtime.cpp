@@ -1,0 +1,237 @@
+// libneptune_hip: hiprtc compile + code-object cache + module launch for gfx950.
+//
+// This is the native half of the operator bridge.  The Python emitter hands over complete HIP
+// source text; this library turns it into a loaded module (replacing the reference's
+// write-file/import/@triton.jit step, neptune_codegen/template.py:198-225) and launches its
+// kernels on the caller's stream (replacing kernel[grid](...), template.py:377-390).
+#include "../../include/neptune_hip.h"
+
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include <sys/stat.h>
+#include <unistd.h>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& message) {
+  g_last_error = message;
+  return code;
+}
+
+int hip_fail(hipError_t err, const char* what) {
+  std::string msg = std::string(what) + " failed: " + hipGetErrorName(err) + " (" +
+                    hipGetErrorString(err) + ")";
+  return fail(NEP_ERR_HIP, msg);
+}
+
+std::vector<std::string> split_options(const char* options) {
+  std::vector<std::string> out;
+  if (options == nullptr) return out;
+  std::string cur;
+  for (const char* p = options;; ++p) {
+    if (*p == '\n' || *p == '\0') {
+      if (!cur.empty()) out.push_back(cur);
+      cur.clear();
+      if (*p == '\0') break;
+    } else {
+      cur.push_back(*p);
+    }
+  }
+  return out;
+}
+
+bool read_file(const char* path, std::vector<char>* out) {
+  FILE* f = std::fopen(path, "rb");
+  if (f == nullptr) return false;
+  std::fseek(f, 0, SEEK_END);
+  long size = std::ftell(f);
+  std::fseek(f, 0, SEEK_SET);
+  if (size <= 0) {
+    std::fclose(f);
+    return false;
+  }
+  out->resize(static_cast<size_t>(size));
+  size_t got = std::fread(out->data(), 1, out->size(), f);
+  std::fclose(f);
+  return got == out->size();
+}
+
+// Write via a temporary file and rename, so a concurrent reader never sees a partial object.
+bool write_file_atomic(const char* path, const void* data, size_t size) {
+  std::string tmp = std::string(path) + ".tmp" + std::to_string(static_cast<long>(getpid()));
+  FILE* f = std::fopen(tmp.c_str(), "wb");
+  if (f == nullptr) return false;
+  size_t put = std::fwrite(data, 1, size, f);
+  bool ok = (put == size) && (std::fclose(f) == 0);
+  if (!ok) {
+    std::remove(tmp.c_str());
+    return false;
+  }
+  return std::rename(tmp.c_str(), path) == 0;
+}
+
+// hiprtc compile of one translation unit to a code object.
+int compile_to_code(const char* source, const char* name, const char* options,
+                    std::vector<char>* code) {
+  hiprtcProgram prog;
+  hiprtcResult r = hiprtcCreateProgram(&prog, source, name ? name : "neptune_kernel.hip", 0,
+                                       nullptr, nullptr);
+  if (r != HIPRTC_SUCCESS)
+    return fail(NEP_ERR_COMPILE, std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r));
+  std::vector<std::string> opts = split_options(options);
+  std::vector<const char*> argv;
+  argv.reserve(opts.size());
+  for (const auto& o : opts) argv.push_back(o.c_str());
+  r = hiprtcCompileProgram(prog, static_cast<int>(argv.size()), argv.data());
+  size_t log_size = 0;
+  hiprtcGetProgramLogSize(prog, &log_size);
+  std::string log;
+  if (log_size > 1) {
+    log.resize(log_size);
+    hiprtcGetProgramLog(prog, &log[0]);
+  }
+  if (r != HIPRTC_SUCCESS) {
+    hiprtcDestroyProgram(&prog);
+    return fail(NEP_ERR_COMPILE, std::string("hiprtc compile of ") + (name ? name : "?") +
+                                     " failed: " + hiprtcGetErrorString(r) + "\n" + log);
+  }
+  size_t code_size = 0;
+  r = hiprtcGetCodeSize(prog, &code_size);
+  if (r != HIPRTC_SUCCESS || code_size == 0) {
+    hiprtcDestroyProgram(&prog);
+    return fail(NEP_ERR_COMPILE, "hiprtc produced no code object");
+  }
+  code->resize(code_size);
+  r = hiprtcGetCode(prog, code->data());
+  hiprtcDestroyProgram(&prog);
+  if (r != HIPRTC_SUCCESS)
+    return fail(NEP_ERR_COMPILE, std::string("hiprtcGetCode: ") + hiprtcGetErrorString(r));
+  return NEP_OK;
+}
+
+// In-process module cache: exact (device, options, source) identity -> loaded module.  Kept
+// for the life of the process, like the reference's generated-module dictionaries.
+std::mutex g_mutex;
+std::map<std::tuple<int, std::string, std::string>, hipModule_t> g_modules;
+
+}  // namespace
+
+extern "C" {
+
+int nep_abi_version(void) { return 1; }
+
+const char* nep_last_error(void) { return g_last_error.c_str(); }
+
+int nep_compile_code_object(const char* source, const char* name, const char* options,
+                            const char* cache_file, void** code_out, size_t* size_out) {
+  if (source == nullptr || code_out == nullptr || size_out == nullptr)
+    return fail(NEP_ERR_INVALID, "nep_compile_code_object: null argument");
+  std::vector<char> code;
+  int rc = compile_to_code(source, name, options, &code);
+  if (rc != NEP_OK) return rc;
+  if (cache_file != nullptr && !write_file_atomic(cache_file, code.data(), code.size()))
+    return fail(NEP_ERR_IO, std::string("cannot write code-object cache ") + cache_file);
+  void* buf = std::malloc(code.size());
+  if (buf == nullptr) return fail(NEP_ERR_INVALID, "out of host memory");
+  std::memcpy(buf, code.data(), code.size());
+  *code_out = buf;
+  *size_out = code.size();
+  g_last_error.clear();
+  return NEP_OK;
+}
+
+void nep_free(void* buffer) { std::free(buffer); }
+
+int nep_compile(const char* source, const char* name, const char* options,
+                const char* cache_file, uint64_t* module_out) {
+  if (source == nullptr || module_out == nullptr)
+    return fail(NEP_ERR_INVALID, "nep_compile: null argument");
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+  auto key = std::make_tuple(device, std::string(options ? options : ""), std::string(source));
+  std::lock_guard<std::mutex> lock(g_mutex);
+  auto it = g_modules.find(key);
+  if (it != g_modules.end()) {
+    *module_out = reinterpret_cast<uint64_t>(it->second);
+    return NEP_OK;
+  }
+  std::vector<char> code;
+  bool from_cache = cache_file != nullptr && read_file(cache_file, &code);
+  if (!from_cache) {
+    int rc = compile_to_code(source, name, options, &code);
+    if (rc != NEP_OK) return rc;
+    // A cache that cannot be written is not an error: the module is still usable.
+    if (cache_file != nullptr) write_file_atomic(cache_file, code.data(), code.size());
+  }
+  hipModule_t module = nullptr;
+  err = hipModuleLoadData(&module, code.data());
+  if (err != hipSuccess && from_cache) {
+    // A stale or foreign cache entry: rebuild from source once before giving up.
+    (void)hipGetLastError();
+    int rc = compile_to_code(source, name, options, &code);
+    if (rc != NEP_OK) return rc;
+    if (cache_file != nullptr) write_file_atomic(cache_file, code.data(), code.size());
+    err = hipModuleLoadData(&module, code.data());
+  }
+  if (err != hipSuccess) return hip_fail(err, "hipModuleLoadData");
+  g_modules.emplace(std::move(key), module);
+  *module_out = reinterpret_cast<uint64_t>(module);
+  g_last_error.clear();
+  return NEP_OK;
+}
+
+int nep_get_kernel(uint64_t module, const char* kernel_name, uint64_t* kernel_out) {
+  if (module == 0 || kernel_name == nullptr || kernel_out == nullptr)
+    return fail(NEP_ERR_INVALID, "nep_get_kernel: null argument");
+  hipFunction_t fn = nullptr;
+  hipError_t err = hipModuleGetFunction(&fn, reinterpret_cast<hipModule_t>(module), kernel_name);
+  if (err != hipSuccess)
+    return hip_fail(err, (std::string("hipModuleGetFunction(") + kernel_name + ")").c_str());
+  *kernel_out = reinterpret_cast<uint64_t>(fn);
+  return NEP_OK;
+}
+
+int nep_launch(uint64_t kernel, const uint32_t grid[3], const uint32_t block[3],
+               uint32_t lds_bytes, void* stream, void** args, size_t nargs) {
+  if (kernel == 0 || grid == nullptr || block == nullptr)
+    return fail(NEP_ERR_INVALID, "nep_launch: null kernel, grid or block");
+  if (nargs != 0 && args == nullptr)
+    return fail(NEP_ERR_INVALID, "nep_launch: nargs > 0 but args is null");
+  if (grid[0] == 0 || grid[1] == 0 || grid[2] == 0)
+    return fail(NEP_ERR_INVALID, "nep_launch: empty grid");
+  if (block[0] * block[1] * block[2] == 0 || block[0] * block[1] * block[2] > 1024)
+    return fail(NEP_ERR_INVALID, "nep_launch: workgroup size must be in [1, 1024]");
+  hipError_t err = hipModuleLaunchKernel(reinterpret_cast<hipFunction_t>(kernel), grid[0],
+                                         grid[1], grid[2], block[0], block[1], block[2],
+                                         lds_bytes, reinterpret_cast<hipStream_t>(stream), args,
+                                         nullptr);
+  if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel");
+  return NEP_OK;
+}
+
+int nep_device_arch(char* buf, size_t buf_len) {
+  if (buf == nullptr || buf_len == 0) return fail(NEP_ERR_INVALID, "nep_device_arch: no buffer");
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+  hipDeviceProp_t prop;
+  err = hipGetDeviceProperties(&prop, device);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDeviceProperties");
+  std::snprintf(buf, buf_len, "%s", prop.gcnArchName);
+  return NEP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,195 @@
+"""ctypes binding to libneptune_hip.so (include/neptune_hip.h).
+
+The library is loaded after torch so that it binds to torch's HIP runtime (both carry the
+SONAME libamdhip64.so.7): device pointers and streams from torch are then valid in it.  There
+is no fallback: without the built library every device entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import os
+import pathlib
+import threading
+
+PACKAGE_DIR = pathlib.Path(__file__).resolve().parent
+LIB_PATH = PACKAGE_DIR / "_lib" / "libneptune_hip.so"
+CACHE_DIR = PACKAGE_DIR / "_codeobj"
+
+NEP_OK = 0
+EXPORTED = ("nep_abi_version", "nep_last_error", "nep_compile", "nep_compile_code_object",
+            "nep_free", "nep_get_kernel", "nep_launch", "nep_device_arch")
+
+_lock = threading.Lock()
+_lib = None
+
+
+class HipError(RuntimeError):
+    """A failure reported by libneptune_hip; the message carries the HIP error name."""
+
+
+def library_path() -> pathlib.Path:
+    return LIB_PATH
+
+
+def load_library(require_torch: bool = True) -> ctypes.CDLL:
+    """Load (once) and type the C ABI.  Raises RuntimeError if the library is not built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if require_torch:
+            import torch  # noqa: F401  -- bind to torch's HIP runtime, see module docstring
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"neptune HIP runtime library is not built ({LIB_PATH}); run "
+                "`python -c 'import __graft_entry__ as g; g.build()'` from the repository root")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        u64p = ctypes.POINTER(ctypes.c_uint64)
+        lib.nep_abi_version.restype = ctypes.c_int
+        lib.nep_last_error.restype = ctypes.c_char_p
+        lib.nep_compile.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+                                    ctypes.c_char_p, u64p]
+        lib.nep_compile.restype = ctypes.c_int
+        lib.nep_compile_code_object.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+                                                ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                                ctypes.POINTER(ctypes.c_size_t)]
+        lib.nep_compile_code_object.restype = ctypes.c_int
+        lib.nep_free.argtypes = [ctypes.c_void_p]
+        lib.nep_free.restype = None
+        lib.nep_get_kernel.argtypes = [ctypes.c_uint64, ctypes.c_char_p, u64p]
+        lib.nep_get_kernel.restype = ctypes.c_int
+        lib.nep_launch.argtypes = [ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint32),
+                                   ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint32,
+                                   ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
+                                   ctypes.c_size_t]
+        lib.nep_launch.restype = ctypes.c_int
+        lib.nep_device_arch.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+        lib.nep_device_arch.restype = ctypes.c_int
+        if lib.nep_abi_version() != 1:
+            raise RuntimeError("libneptune_hip ABI version mismatch; rebuild the library")
+        _lib = lib
+        return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != NEP_OK:
+        msg = _lib.nep_last_error().decode(errors="replace") if _lib is not None else ""
+        raise HipError(f"{what}: {msg}")
+
+
+def runtime_identity() -> str:
+    """What a code object depends on besides its source: the hiprtc that compiled it."""
+    import torch
+
+    return f"hiprtc-torch-{torch.version.hip}"
+
+
+def cache_key(source: str, options: tuple[str, ...]) -> str:
+    h = hashlib.sha256()
+    for part in (runtime_identity(), "\n".join(options), source):
+        h.update(part.encode())
+        h.update(b"\0")
+    return h.hexdigest()
+
+
+def _cache_file(source: str, options: tuple[str, ...]) -> pathlib.Path:
+    return CACHE_DIR / f"{cache_key(source, options)[:40]}.co"
+
+
+def compile_code_object(source: str, name: str, options: tuple[str, ...],
+                        write_cache: bool = True) -> int:
+    """hiprtc compile without a GPU; returns the code-object size.  Raises HipError."""
+    lib = load_library()
+    path = None
+    if write_cache:
+        CACHE_DIR.mkdir(parents=True, exist_ok=True)
+        path = str(_cache_file(source, options)).encode()
+    buf = ctypes.c_void_p()
+    size = ctypes.c_size_t()
+    rc = lib.nep_compile_code_object(source.encode(), name.encode(), "\n".join(options).encode(),
+                                     path, ctypes.byref(buf), ctypes.byref(size))
+    _check(rc, f"compile {name}")
+    lib.nep_free(buf)
+    return size.value
+
+
+def load_module(source: str, name: str, options: tuple[str, ...]) -> int:
+    """Compile (or load from the on-disk cache) and load on the current device."""
+    lib = load_library()
+    CACHE_DIR.mkdir(parents=True, exist_ok=True)
+    path = str(_cache_file(source, options)).encode()
+    handle = ctypes.c_uint64()
+    rc = lib.nep_compile(source.encode(), name.encode(), "\n".join(options).encode(), path,
+                         ctypes.byref(handle))
+    _check(rc, f"compile/load {name}")
+    return handle.value
+
+
+def get_kernel(module: int, kernel_name: str) -> int:
+    lib = load_library()
+    handle = ctypes.c_uint64()
+    _check(lib.nep_get_kernel(module, kernel_name.encode(), ctypes.byref(handle)),
+           f"kernel {kernel_name}")
+    return handle.value
+
+
+# argument kinds of kernel signatures
+PTR, I64, I32, F32 = ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_float
+
+
+class Kernel:
+    """A loaded extern "C" kernel with a fixed argument signature."""
+
+    __slots__ = ("handle", "name", "argtypes", "block", "lds")
+
+    def __init__(self, handle: int, name: str, argtypes: tuple, block: int, lds: int = 0):
+        self.handle, self.name, self.argtypes, self.block, self.lds = handle, name, argtypes, block, lds
+
+    def launch(self, grid, args, stream: int) -> None:
+        if len(args) != len(self.argtypes):
+            raise TypeError(f"{self.name}: expected {len(self.argtypes)} arguments, got {len(args)}")
+        values = [t(a) for t, a in zip(self.argtypes, args)]
+        ptrs = (ctypes.c_void_p * len(values))(*[ctypes.addressof(v) for v in values])
+        g = (ctypes.c_uint32 * 3)(*(tuple(int(d) for d in grid) + (1, 1, 1))[:3])
+        b = (ctypes.c_uint32 * 3)(self.block, 1, 1)
+        rc = _lib.nep_launch(self.handle, g, b, self.lds, ctypes.c_void_p(stream), ptrs, len(values))
+        _check(rc, f"launch {self.name}")
+
+
+class Program:
+    """One generated unit: compiled and loaded lazily per device, kernels fetched by name."""
+
+    def __init__(self, source: str, name: str, options: tuple[str, ...]):
+        self.source, self.name, self.options = source, name, tuple(options)
+        self._modules: dict[int, int] = {}
+        self._kernels: dict[tuple, Kernel] = {}
+
+    def kernel(self, kernel_name: str, argtypes: tuple, block: int, device: int) -> Kernel:
+        key = (device, kernel_name)
+        k = self._kernels.get(key)
+        if k is not None:
+            return k
+        import torch
+
+        with torch.cuda.device(device):
+            module = self._modules.get(device)
+            if module is None:
+                module = load_module(self.source, self.name, self.options)
+                self._modules[device] = module
+            k = Kernel(get_kernel(module, kernel_name), kernel_name, argtypes, block)
+        self._kernels[key] = k
+        return k
+
+    def precompile(self) -> int:
+        """Fill the on-disk code-object cache (no GPU needed)."""
+        path = _cache_file(self.source, self.options)
+        if path.exists() and path.stat().st_size > 0:
+            return path.stat().st_size
+        return compile_code_object(self.source, self.name, self.options)
+
+
+def current_stream(device) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

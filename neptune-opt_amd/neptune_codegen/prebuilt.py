@@ -1,0 +1,58 @@
+"""Kernel units behind the benchmark configurations, enumerated without a GPU.
+
+Launch-shape selection only reads shapes, strides, dtypes and pointer alignment, so meta
+tensors (data pointer 0, always aligned) reproduce the variants a real launch picks.
+"""
+from __future__ import annotations
+
+
+def _fold_programs():
+    import torch
+
+    from neptune_codegen.autotune import best_config
+    from neptune_codegen.skeleton import param_defaults
+    from neptune_codegen.template import _fold_variant, compile_skeleton
+
+    out = []
+    lse = param_defaults("logsumexp")
+    shapes = [(8192, 1024, torch.float32)] + [(16384, w, torch.bfloat16) for w in (128, 1000, 4096, 32000)]
+    for rows, ncols, dtype in shapes:
+        x2 = torch.empty((rows, ncols), device="meta", dtype=dtype)
+        block, warps = best_config(rows, ncols, dtype, None)
+        var = _fold_variant(x2, ncols, block, warps)
+        out.append(compile_skeleton("logsumexp", lse).program(var))
+    x2 = torch.empty((64, 262144), device="meta", dtype=torch.bfloat16)
+    partial, _merge = compile_skeleton("logsumexp", lse, plan="split")
+    out.append(partial.program(_fold_variant(x2, 262144, 1024, 4, split_block=1024)))
+    return out
+
+
+def _row_programs():
+    import torch
+
+    from neptune_codegen.template import _row_variant, compile_state_reduction
+
+    out = []
+    x = torch.empty((32768, 4096), device="meta", dtype=torch.bfloat16)
+    g = torch.empty((4096,), device="meta", dtype=torch.bfloat16)
+    out.append(compile_state_reduction("rms_norm", {"eps": 1e-6}).program(_row_variant(x, g, 4096)))
+    out.append(compile_state_reduction("l2_normalize", {"eps": 1e-6}).program(_row_variant(x, None, 4096)))
+    return out
+
+
+def _segment_programs():
+    import torch
+
+    from neptune_codegen.torch_op import _segment_variant, compile_segment_reduction
+
+    out = []
+    data = torch.empty((1310720, 128), device="meta", dtype=torch.float16)
+    spans = torch.empty((65537,), device="meta", dtype=torch.int32)
+    for name in ("segment_sum", "segment_mean"):
+        prog = compile_segment_reduction(name, {"offsets": True})
+        out.append(prog.program(_segment_variant(data, spans, 128)))
+    return out
+
+
+def programs():
+    return _fold_programs() + _row_programs() + _segment_programs()

@@ -1,0 +1,419 @@
+"""Plans, validation, compilation caches and the launch ABI of the HIP backend.
+
+Mirrors the reference's neptune_codegen/template.py: the same plan names and split capacity
+(validate_plan :109-111, split_launch_shape :114-125), the same row-last contract and refusals
+(_validate_row_last :338-352, _row_last_layout :355-365, validate_rms_inputs :267-291), the
+same direct entry points (run :393-442, run_rms_norm :322-335) and the same ownership rule:
+torch allocates every output and scratch buffer, kernels never allocate.  What differs is
+below the launch: generated HIP units compiled by hiprtc and launched through
+libneptune_hip on the caller's current stream.
+"""
+from __future__ import annotations
+
+import math
+import threading
+
+from neptune_codegen import hip
+from neptune_codegen.autotune import (UNROLL, best_config, lanes_per_row, parameter_identity,
+                                      parameter_tag, vec_of)
+from neptune_codegen.emitters import (BASE_OPTIONS, NO_CONTRACT, FoldVariant, RowVariant,
+                                      check_supported, emit_kernel_source, emit_rms_state_source,
+                                      fold_kernel_name, rms_kernel_names)
+from neptune_codegen.skeleton import SKELETONS, all_registered
+
+MAX_SPLIT_PARTS = 4096
+_CACHE: dict = {}
+_STATE_CACHE: dict = {}
+_cache_lock = threading.Lock()
+
+
+def validate_plan(plan: str) -> None:
+    if plan not in ("serial", "split"):
+        raise ValueError(f"unknown reduction plan {plan!r}; expected 'serial' or 'split'")
+
+
+def split_launch_shape(ncols, block: int) -> tuple[int, int]:
+    """(nparts, merge width) of an explicit split; refuses symbolic width and over-capacity."""
+    if type(ncols) is not int:
+        raise NotImplementedError("explicit split requires a concrete width; use plan='serial' for dynamic width")
+    if type(block) is not int or block <= 0 or block & (block - 1):
+        raise ValueError("split BLOCK must be a positive power of two")
+    if ncols <= 0:
+        raise ValueError("split requires positive width")
+    nparts = (ncols + block - 1) // block
+    if nparts > MAX_SPLIT_PARTS:
+        raise NotImplementedError(f"split needs {nparts} partials, exceeding capacity {MAX_SPLIT_PARTS}; use serial")
+    return nparts, 1 << (nparts - 1).bit_length()
+
+
+def _validate_row_last(x, *, metadata: bool = False):
+    import torch
+
+    if x.layout != torch.strided:
+        raise TypeError("Neptune requires a strided tensor")
+    if x.ndim < 1:
+        raise ValueError("Neptune row-last reductions require rank >= 1")
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"unsupported Neptune dtype {x.dtype}; expected float16/bfloat16/float32")
+    if not metadata and x.device.type != "cuda":
+        raise ValueError(f"unsupported Neptune device {x.device}; execution requires a ROCm (cuda) device")
+    torch._check(x.shape[-1] > 0, lambda: "Neptune requires positive last-dimension width")
+
+
+def _row_last_layout(x):
+    """Flatten leading dimensions only; reshape copies exactly when no view exists."""
+    rows = 1
+    for size in x.shape[:-1]:
+        rows = rows * size
+    ncols = x.shape[-1]
+    return x.reshape(rows, ncols), rows, ncols
+
+
+# ---------------------------------------------------------------- compiled programs
+class FoldProgram:
+    """The generated kernels of one (skeleton, parameters, plan[, stage]); variants compile
+    lazily, one hiprtc unit per launch shape."""
+
+    def __init__(self, name: str, values: dict, plan: str, stage: str = ""):
+        self.name, self.values, self.plan, self.stage = name, dict(values), plan, stage
+        self.sk = SKELETONS[name]
+        self._programs: dict = {}
+
+    def source(self, var: FoldVariant) -> str:
+        return emit_kernel_source(self.sk, self.values, plan=self.plan, variants=(var,))
+
+    def program(self, var: FoldVariant) -> hip.Program:
+        prog = self._programs.get(var)
+        if prog is None:
+            prog = hip.Program(self.source(var), f"{self.name}_{self.plan}_{var.tag()}.hip",
+                               BASE_OPTIONS)
+            self._programs[var] = prog
+        return prog
+
+    def kernel(self, var: FoldVariant, stage: str, device: int) -> hip.Kernel:
+        name = fold_kernel_name(self.sk, self.plan, stage, var)
+        if stage == "partial":
+            args = (hip.PTR,) * 5 + (hip.I64,) * 6
+            block = var.wg
+        elif stage == "merge":
+            args = (hip.PTR,) * 5 + (hip.I64,) * 3
+            block = 256
+        else:
+            args = (hip.PTR, hip.PTR) + (hip.I64,) * 4
+            block = var.wg
+        return self.program(var).kernel(name, args, block, device)
+
+
+def compile_skeleton(name: str, values: dict | None = None, force: bool = False, *,
+                     plan: str = "serial"):
+    """Generate the fold for (name, values, plan): a FoldProgram, or (partial, merge) for split."""
+    validate_plan(plan)
+    key = (name, parameter_identity(values), plan)
+    with _cache_lock:
+        if not force and key in _CACHE:
+            return _CACHE[key]
+    if name not in SKELETONS:
+        raise KeyError(f"unknown skeleton {name!r}; have {all_registered()}")
+    sk = SKELETONS[name]
+    check_supported(sk)
+    # emit once now so that refusals (missing parameter, split of a two-pass fold, an
+    # uncertified merge) surface at compile time, before any launch
+    emit_kernel_source(sk, values, plan=plan)
+    if plan == "serial":
+        kernel = FoldProgram(name, values or {}, plan)
+    else:
+        shared = FoldProgram(name, values or {}, plan)
+        kernel = (shared, shared)
+    with _cache_lock:
+        _CACHE[key] = kernel
+    return kernel
+
+
+def generated_path(name: str, values: dict | None = None, *, plan: str = "serial") -> str:
+    """Identifier of one generated unit family (kept for API parity; units live in memory
+    and in the code-object cache, keyed by their exact source)."""
+    validate_plan(plan)
+    suffix = "" if plan == "serial" else "_plan_split"
+    return f"neptune_gen_{name}{parameter_tag(values)}{suffix}.hip"
+
+
+# ---------------------------------------------------------------- scalar launch ABI
+def _is_vector(x2, ncols: int, vec: int, extra_align: int = 0) -> bool:
+    if x2.dim() != 2:
+        return False
+    col_ok = x2.stride(1) == 1 or ncols == 1
+    return (col_ok and x2.stride(0) % vec == 0 and ncols % vec == 0
+            and x2.data_ptr() % 16 == 0 and (extra_align == 0 or extra_align % vec == 0))
+
+
+def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: int = 0) -> FoldVariant:
+    """Launch shape: 16-byte loads when the layout allows, lanes per row from BLOCK,
+    workgroup = max(64 * num_warps, lanes per row)."""
+    vec = vec_of(x2.dtype)
+    vector = _is_vector(x2, ncols, vec, split_block)
+    if vector and split_block and split_block < vec:
+        vector = False
+    tpr = lanes_per_row(block, vec if vector else 1)
+    waves = max(1, min(16, int(num_warps)))
+    waves = 1 << (waves - 1).bit_length()
+    return FoldVariant(str(x2.dtype).replace("torch.", ""), vector, tpr, UNROLL, waves)
+
+
+def _grid_1d(items: int, per_wg: int) -> int:
+    return max(1, (items + per_wg - 1) // per_wg)
+
+
+def launch_reduction(kernel, plan, x2, out, rows, ncols, block, num_warps, *, wrapper=None):
+    """Launch a compiled fold on the current stream; scratch for split is torch-allocated."""
+    import torch
+
+    validate_plan(plan)
+    device = x2.device.index if x2.device.index is not None else torch.cuda.current_device()
+    stream = hip.current_stream(x2.device)
+    if plan == "serial":
+        var = _fold_variant(x2, ncols, block, num_warps)
+        k = kernel.kernel(var, "", device)
+        rpw = max(1, var.wg // var.tpr)
+        k.launch((_grid_1d(rows, rpw),),
+                 (x2.data_ptr(), out.data_ptr(), rows, ncols, x2.stride(0), x2.stride(1)), stream)
+        return
+    nparts, _merge = split_launch_shape(ncols, block)
+    partial_m = torch.empty((rows, nparts), device=x2.device, dtype=torch.float32)
+    partial_a = torch.empty((rows, nparts), device=x2.device, dtype=torch.float32)
+    partial_v = torch.empty((rows, nparts), device=x2.device, dtype=torch.int32)
+    partial_s = torch.empty((rows, nparts), device=x2.device, dtype=torch.int32)
+    partial, merge = kernel
+    var = _fold_variant(x2, ncols, block, num_warps, split_block=block)
+    kp = partial.kernel(var, "partial", device)
+    rpw = max(1, var.wg // var.tpr)
+    kp.launch((_grid_1d(rows * nparts, rpw),),
+              (x2.data_ptr(), partial_m.data_ptr(), partial_a.data_ptr(), partial_v.data_ptr(),
+               partial_s.data_ptr(), rows, ncols, x2.stride(0), x2.stride(1), nparts, block),
+              stream)
+    km = merge.kernel(var, "merge", device)
+    km.launch((_grid_1d(rows, 4),),
+              (partial_m.data_ptr(), partial_a.data_ptr(), partial_v.data_ptr(),
+               partial_s.data_ptr(), out.data_ptr(), rows, ncols, nparts), stream)
+
+
+def run(name: str, x, block: int | None = None, num_warps: int | None = None,
+        keepdim: bool = False, plan: str = "serial", **params):
+    """Reduce the last dimension of `x` with the generated fold `name`.
+
+    Rank >= 1 returns x.shape[:-1] (keepdim appends a 1).  Real execution needs a ROCm device
+    and float16/bfloat16/float32; Fake/meta tensors return metadata only.  Declared parameter
+    defaults are filled for anything not passed.
+    """
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensor
+
+    from neptune_codegen.skeleton import param_defaults
+
+    metadata = isinstance(x, FakeTensor) or x.device.type == "meta"
+    _validate_row_last(x, metadata=metadata)
+    params = {**param_defaults(name), **(params or {})}
+    validate_plan(plan)
+    if plan == "split":
+        block = 1024 if block is None else block
+        num_warps = 4 if num_warps is None else num_warps
+        from neptune_codegen.algebra import derive_merge_certificate
+
+        derive_merge_certificate(SKELETONS[name], params)
+        split_launch_shape(x.shape[-1], block)
+    shape = x.shape[:-1] + ((1,) if keepdim else ())
+    out = torch.empty(shape, device=x.device, dtype=x.dtype)
+    if metadata:
+        return out
+    x2, rows, ncols = _row_last_layout(x)
+    if isinstance(rows, int) and rows == 0:
+        return out
+    kernel = compile_skeleton(name, params, plan=plan)
+    if block is None or num_warps is None:
+        cfg = best_config(rows, ncols, x.dtype, x.device)
+        block = cfg[0] if block is None else block
+        num_warps = cfg[1] if num_warps is None else num_warps
+    launch_reduction(kernel, plan, x2, out, rows, ncols, block, num_warps)
+    return out
+
+
+# ---------------------------------------------------------------- structured RMS / L2
+class RowProgram:
+    """Generated structured-state kernels of one (spec, eps, plan)."""
+
+    def __init__(self, spec_name: str, params: dict, plan: str):
+        self.spec_name, self.params, self.plan = spec_name, dict(params), plan
+        self._programs: dict = {}
+
+    def source(self, var: RowVariant) -> str:
+        from neptune_codegen.skeleton import state_reduction_spec
+
+        return emit_rms_state_source(state_reduction_spec(self.spec_name), self.params,
+                                     plan=self.plan, variants=(var,))
+
+    def program(self, var: RowVariant) -> hip.Program:
+        prog = self._programs.get(var)
+        if prog is None:
+            prog = hip.Program(self.source(var), f"{self.spec_name}_{self.plan}_{var.tag()}.hip",
+                               BASE_OPTIONS + NO_CONTRACT)
+            self._programs[var] = prog
+        return prog
+
+    def kernels(self, var: RowVariant, device: int) -> tuple:
+        names = rms_kernel_names(self.spec_name, self.plan, var)
+        prog = self.program(var)
+        if self.plan == "serial":
+            return (prog.kernel(names[0], (hip.PTR,) * 3 + (hip.I64,) * 5, var.wg, device),)
+        return (prog.kernel(names[0], (hip.PTR,) * 3 + (hip.I64,) * 6, var.wg, device),
+                prog.kernel(names[1], (hip.PTR,) * 5 + (hip.I64,) * 7, var.wg, device))
+
+
+def compile_state_reduction(name: str, params=None, *, plan: str = "serial"):
+    """Compile a certified structured backend (RMSNorm, L2-normalize)."""
+    from neptune_codegen.algebra import derive_state_certificate
+    from neptune_codegen.skeleton import state_reduction_spec
+
+    validate_plan(plan)
+    if name not in ("rms_norm", "l2_normalize"):
+        raise NotImplementedError("this structured compiler implements RMSNorm and L2-normalize; "
+                                  "segments use the serial backend")
+    params = dict(params or {})
+    spec = state_reduction_spec(name)
+    derive_state_certificate(spec)
+    emit_rms_state_source(spec, params, plan=plan)  # validates even on a cache hit
+    key = (spec, parameter_identity(params), plan)
+    with _cache_lock:
+        if key not in _STATE_CACHE:
+            _STATE_CACHE[key] = RowProgram(name, params, plan)
+        return _STATE_CACHE[key]
+
+
+def _check_eps(params):
+    eps = params.get("eps")
+    if params.keys() != {"eps"} or type(eps) not in (int, float) or not math.isfinite(eps) or eps <= 0:
+        raise ValueError("RMSNorm requires an explicit finite positive eps")
+
+
+def validate_rms_inputs(x, gamma, params=None, *, plan="serial", metadata=False):
+    """Full-vector RMSNorm contract (template.py:267-291); symbolic batch survives."""
+    import torch
+
+    validate_plan(plan)
+    _validate_row_last(x, metadata=metadata)
+    params = dict(params or {})
+    _check_eps(params)
+    if gamma.layout != torch.strided or gamma.ndim != 1:
+        raise ValueError("RMSNorm gamma must be a strided 1D tensor")
+    if gamma.dtype != x.dtype or gamma.device != x.device:
+        raise ValueError("RMSNorm gamma dtype/device must match input")
+    torch._check(gamma.shape[0] == x.shape[-1], lambda: "RMSNorm gamma width must match input")
+    _check_static_width(x, plan)
+    return x.shape
+
+
+def validate_l2_inputs(x, params=None, *, plan="serial", metadata=False):
+    """L2-normalize contract: the RMS row-last rules without gamma."""
+    validate_plan(plan)
+    _validate_row_last(x, metadata=metadata)
+    _check_eps(dict(params or {}))
+    _check_static_width(x, plan)
+    return x.shape
+
+
+def _check_static_width(x, plan):
+    if type(x.shape[-1]) is not int:
+        raise NotImplementedError("RMSNorm first backend requires a static feature width")
+    if plan == "serial" and x.shape[-1] > 32768:
+        raise NotImplementedError("resident RMSNorm width exceeds 32768; request split explicitly")
+    if plan == "split":
+        split_launch_shape(x.shape[-1], 1024)
+
+
+def _row_variant(flat, gamma, width: int, *, tile: int | None = None) -> RowVariant:
+    vec = vec_of(flat.dtype)
+    vector = _is_vector(flat, width, vec, tile or 0)
+    if vector and gamma is not None:
+        vector = gamma.stride(0) == 1 and gamma.data_ptr() % 16 == 0
+    span = tile if tile is not None else width
+    slots = (span + vec - 1) // vec if vector else span
+    nv = 8 if vector else 16
+    if tile is not None:
+        nv = 2 if vector else 8
+    tpr = 1 << max(0, (max(1, -(-slots // nv)) - 1).bit_length())
+    while tpr > 1024:
+        nv *= 2
+        tpr = 1 << max(0, (max(1, -(-slots // nv)) - 1).bit_length())
+    nv = max(1, min(nv, -(-slots // tpr)))
+    nv = 1 << (nv - 1).bit_length()
+    return RowVariant(str(flat.dtype).replace("torch.", ""), vector, tpr, nv)
+
+
+def _persistent_grid(items_per_wg: int, items: int, device) -> int:
+    import torch
+
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    return max(1, min(_grid_1d(items, items_per_wg), cus * 8))
+
+
+def launch_rms_norm(kernel, x, gamma, out, *, plan="serial", wrapper=None):
+    """Shared launch of the structured RMS / L2 kernels; scratch is torch-allocated."""
+    import torch
+
+    flat, rows, width = _row_last_layout(x)
+    if isinstance(rows, int) and rows == 0:
+        return
+    device = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    stream = hip.current_stream(x.device)
+    g_ptr = gamma.data_ptr() if gamma is not None else 0
+    g_stride = gamma.stride(0) if gamma is not None else 0
+    if plan == "serial":
+        var = _row_variant(flat, gamma, width)
+        (k,) = kernel.kernels(var, device)
+        rpw = max(1, var.wg // var.tpr)
+        k.launch((_persistent_grid(rpw, rows, x.device),),
+                 (flat.data_ptr(), g_ptr, out.data_ptr(), rows, width, flat.stride(0),
+                  flat.stride(1), g_stride), stream)
+        return
+    parts, _ = split_launch_shape(width, 1024)
+    totals = torch.empty((rows, parts), device=x.device, dtype=torch.float32)
+    counts = torch.empty((rows, parts), device=x.device, dtype=torch.int64)
+    var = _row_variant(flat, gamma, width, tile=1024)
+    kp, km = kernel.kernels(var, device)
+    rpw = max(1, var.wg // var.tpr)
+    grid = _persistent_grid(rpw, rows * parts, x.device)
+    kp.launch((grid,), (flat.data_ptr(), totals.data_ptr(), counts.data_ptr(), rows, width,
+                        flat.stride(0), flat.stride(1), parts, 1024), stream)
+    km.launch((grid,), (flat.data_ptr(), g_ptr, totals.data_ptr(), counts.data_ptr(),
+                        out.data_ptr(), rows, width, flat.stride(0), flat.stride(1), g_stride,
+                        parts, 1024), stream)
+
+
+def run_rms_norm(x, gamma, *, eps: float = 1e-6, plan="serial"):
+    """Full-vector RMSNorm over the last dimension; fresh contiguous output in x.dtype."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensor
+
+    params = {"eps": eps}
+    metadata = isinstance(x, FakeTensor) or x.device.type == "meta"
+    shape = validate_rms_inputs(x, gamma, params, plan=plan, metadata=metadata)
+    out = torch.empty(shape, device=x.device, dtype=x.dtype)
+    if metadata or x.numel() == 0:
+        return out
+    kernel = compile_state_reduction("rms_norm", params, plan=plan)
+    launch_rms_norm(kernel, x, gamma, out, plan=plan)
+    return out
+
+
+def run_l2_normalize(x, *, eps: float = 1e-6, plan="serial"):
+    """x / max(||x||_2, eps) over the last dimension (fp32 statistics, dtype output)."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensor
+
+    params = {"eps": eps}
+    metadata = isinstance(x, FakeTensor) or x.device.type == "meta"
+    shape = validate_l2_inputs(x, params, plan=plan, metadata=metadata)
+    out = torch.empty(shape, device=x.device, dtype=x.dtype)
+    if metadata or x.numel() == 0:
+        return out
+    kernel = compile_state_reduction("l2_normalize", params, plan=plan)
+    launch_rms_norm(kernel, x, None, out, plan=plan)
+    return out

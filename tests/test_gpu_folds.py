@@ -1,0 +1,146 @@
+"""GPU parity of the scalar folds (serial, split, two-pass) against the CPU oracle.
+
+Tolerances are BASELINE.json's: fp32 rtol 1e-5 / atol 1e-6; bf16/fp16 rtol 1.6e-2 / atol 1e-3.
+Inputs are generated on the CPU from fixed seeds and copied to the device, so the oracle and
+the kernel see identical values.
+"""
+import math
+
+import pytest
+import torch
+
+import neptune_codegen as CG
+from oracle import references as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: (1e-5, 1e-6), torch.bfloat16: (1.6e-2, 1e-3), torch.float16: (1.6e-2, 1e-3)}
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a ROCm GPU")
+    return torch.device("cuda:0")
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _check(name, x_cpu, got, **params):
+    """BASELINE tolerance, plus a tight check: within one ulp of the storage dtype of the fp32
+    oracle (the kernel accumulates in fp32 and rounds once), which a permuted or dropped
+    element would fail even where the BASELINE tolerance would not."""
+    want = R.reference(name, x_cpu, **params)
+    rtol, atol = TOL[x_cpu.dtype]
+    got = got.cpu().float().reshape(want.shape)
+    torch.testing.assert_close(got, want.to(x_cpu.dtype).float() if x_cpu.dtype != torch.float32 else want,
+                               rtol=rtol, atol=atol)
+    if x_cpu.dtype != torch.float32:
+        ulp = torch.finfo(x_cpu.dtype).eps
+        torch.testing.assert_close(got, want, rtol=ulp, atol=1e-6)
+
+
+def test_cfg1_logsumexp_fp32_seed0():
+    dev = _dev()
+    g = torch.Generator().manual_seed(0)
+    x = 3 * torch.randn(8192, 1024, generator=g)
+    _say("cfg1 logsumexp fp32 [8192,1024]")
+    _check("logsumexp", x, CG.run("logsumexp", x.to(dev)))
+
+
+@pytest.mark.parametrize("width", [128, 1000, 4096, 32000])
+def test_cfg2_logsumexp_bf16_widths(width):
+    dev = _dev()
+    g = torch.Generator().manual_seed(1)
+    rows = 16384 if width <= 4096 else 2048
+    x = (4 * torch.randn(rows, width, generator=g)).bfloat16()
+    _say(f"cfg2 logsumexp bf16 [{rows},{width}]")
+    _check("logsumexp", x, CG.run("logsumexp", x.to(dev)))
+
+
+def test_cfg2_split_bf16():
+    dev = _dev()
+    g = torch.Generator().manual_seed(2)
+    x = (4 * torch.randn(64, 262144, generator=g)).bfloat16()
+    _say("cfg2 split logsumexp bf16 [64,262144]")
+    _check("logsumexp", x, CG.run("logsumexp", x.to(dev), plan="split"))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("name", sorted(CG.supported()))
+@pytest.mark.parametrize("plan", ["serial", "split"])
+def test_every_skeleton_every_dtype(name, dtype, plan):
+    dev = _dev()
+    sk = CG.SKELETONS[name]
+    if plan == "split" and sk.two_pass:
+        pytest.skip("two-pass folds refuse the split plan")
+    g = torch.Generator().manual_seed(7)
+    for rows, width in ((5, 1), (33, 77), (16, 1000), (3, 5000)):
+        x = torch.randn(rows, width, generator=g)
+        if name in ("stable_l2", "sumsq_div", "linear_attn", "decay_renorm"):
+            x = x.abs() + 0.1
+        x = x.to(dtype)
+        params = {"eps": 1e-6} if name == "rmsnorm_max" else {}
+        _say(f"skeleton {name} {dtype} {plan} [{rows},{width}]")
+        got = CG.run(name, x.to(dev), plan=plan, block=256 if plan == "split" else None, **params)
+        want = R.reference(name, x, **params)
+        rtol, atol = TOL[dtype]
+        if dtype == torch.float32 and name in ("variance", "std", "sumsq_div", "linear_attn",
+                                               "decay_renorm", "stable_l2", "rmsnorm_max"):
+            rtol = R.summation_tolerance(dtype, width)
+        torch.testing.assert_close(got.cpu().float(), want.to(dtype).float(), rtol=rtol, atol=atol)
+        if dtype != torch.float32:
+            torch.testing.assert_close(got.cpu().float(), want, rtol=torch.finfo(dtype).eps, atol=1e-5)
+
+
+def test_strided_views_and_keepdim():
+    dev = _dev()
+    g = torch.Generator().manual_seed(3)
+    base = torch.randn(6, 40, 24, generator=g)
+    base_dev = base.to(dev)
+    views = [lambda b: b[:, :, ::2], lambda b: b.transpose(1, 2), lambda b: b[:, 3, :],
+             lambda b: b.transpose(0, 2)[1:], lambda b: b[:, :, 1:]]
+    for i, view in enumerate(views):
+        v = view(base)
+        for keep in (False, True):
+            _say(f"strided view {i} keepdim={keep} shape={tuple(v.shape)} stride={v.stride()}")
+            got = CG.run("logsumexp", view(base_dev), keepdim=keep)
+            want = torch.logsumexp(v, dim=-1, keepdim=keep)
+            assert got.shape == want.shape
+            torch.testing.assert_close(got.cpu(), want, rtol=1e-5, atol=1e-6)
+
+
+def test_logsumexp_nonfinite_status_rows():
+    dev = _dev()
+    inf, nan = float("inf"), float("nan")
+    rows = [[nan, inf, 1.0], [inf, -inf, 1.0], [-inf, -inf, -inf], [0.0, -100.0, -200.0],
+            [nan, -inf, -inf], [1.0, 2.0, inf], [-inf, 1.0, -inf]]
+    for plan in ("serial", "split"):
+        for dtype in (torch.float32, torch.bfloat16):
+            x = torch.tensor(rows, dtype=dtype)
+            # widen each row so the nonfinite values land in different lanes and tiles
+            wide = torch.full((len(rows), 3000), -inf, dtype=dtype)
+            wide[:, ::1000] = x
+            for t in (x, wide):
+                _say(f"nonfinite {plan} {dtype} width={t.shape[1]}")
+                got = CG.run("logsumexp", t.to(dev), plan=plan, block=256 if plan == "split" else None)
+                want = torch.logsumexp(t.float(), dim=-1).to(dtype)
+                torch.testing.assert_close(got.cpu(), want, equal_nan=True, rtol=1e-5, atol=1e-6)
+
+
+def test_empty_rows_and_rank1():
+    dev = _dev()
+    assert CG.run("logsumexp", torch.empty(0, 8, device=dev)).shape == (0,)
+    x = torch.randn(9)
+    got = CG.run("logsumexp", x.to(dev))
+    assert got.shape == ()
+    assert math.isclose(float(got), float(torch.logsumexp(x, 0)), rel_tol=1e-5)
+
+
+def test_custom_op_registration_runs_hip():
+    dev = _dev()
+    op = CG.op_handle("lse_scaled", params={"T": 3.0})
+    x = torch.randn(4, 300)
+    got = op(x.to(dev))
+    torch.testing.assert_close(got.cpu(), torch.logsumexp(x / 3.0, -1), rtol=1e-5, atol=1e-6)

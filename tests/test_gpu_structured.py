@@ -1,0 +1,126 @@
+"""GPU parity of RMSNorm, L2-normalize and segment pooling.
+
+RMS/L2: bf16 rtol 1.6e-2 / atol 1e-3 (fp32: 1e-5 / 1e-6) against the canonical fp32-staged
+eager forms.  Segment pooling: bit-exact (NaN positions equal) against torch.segment_reduce on
+the CPU, over the reference's own case table (tests/test_autotune.py:793-833).
+"""
+import pytest
+import torch
+
+import neptune_codegen as CG
+from oracle import references as R
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.float32: (1e-5, 1e-6), torch.bfloat16: (1.6e-2, 1e-3), torch.float16: (1.6e-2, 1e-3)}
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a ROCm GPU")
+    return torch.device("cuda:0")
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _bits_equal(a, b):
+    assert a.shape == b.shape and a.dtype == b.dtype
+    an, bn = torch.isnan(a), torch.isnan(b)
+    assert torch.equal(an, bn), "NaN positions differ"
+    a, b = a.masked_fill(an, 0), b.masked_fill(bn, 0)
+    ia = a.view(torch.int16 if a.element_size() == 2 else torch.int32)
+    ib = b.view(torch.int16 if b.element_size() == 2 else torch.int32)
+    assert torch.equal(ia, ib), f"{(ia != ib).sum().item()} elements differ bitwise"
+
+
+@pytest.mark.parametrize("plan", ["serial", "split"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_rms_norm_parity(dtype, plan):
+    dev = _dev()
+    g = torch.Generator().manual_seed(3)
+    for rows, width in ((64, 4096), (7, 1000), (3, 1), (5, 20000)):
+        x = torch.randn(rows, width, generator=g).to(dtype)
+        gamma = (1 + 0.1 * torch.randn(width, generator=g)).to(dtype)
+        _say(f"rms {dtype} {plan} [{rows},{width}]")
+        got = CG.run_rms_norm(x.to(dev), gamma.to(dev), eps=1e-6, plan=plan)
+        want = R.rms_norm_reference(x, gamma, 1e-6)
+        rtol, atol = TOL[dtype]
+        torch.testing.assert_close(got.cpu().float(), want.float(), rtol=rtol, atol=atol)
+        _say(f"l2 {dtype} {plan} [{rows},{width}]")
+        got = CG.run_l2_normalize(x.to(dev), eps=1e-6, plan=plan)
+        want = R.l2_normalize_reference(x, 1e-6)
+        torch.testing.assert_close(got.cpu().float(), want.float(), rtol=rtol, atol=atol)
+
+
+def test_rms_cfg3_shape_and_strided_gamma():
+    dev = _dev()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(32768, 4096, generator=g).bfloat16()
+    gamma = (1 + 0.1 * torch.randn(4096, generator=g)).bfloat16()
+    _say("cfg3 rms [32768,4096] bf16")
+    got = CG.run_rms_norm(x.to(dev), gamma.to(dev), eps=1e-6).cpu()
+    want = R.rms_norm_reference(x, gamma, 1e-6)
+    torch.testing.assert_close(got.float(), want.float(), rtol=1.6e-2, atol=1e-3)
+    _say("strided x and gamma")
+    xs = torch.randn(16, 2048, generator=g).bfloat16()
+    gs = (1 + 0.1 * torch.randn(2048, generator=g)).bfloat16()
+    got = CG.run_rms_norm(xs.to(dev)[:, ::2], gs.to(dev)[::2], eps=1e-5).cpu()
+    want = R.rms_norm_reference(xs[:, ::2], gs[::2], 1e-5)
+    torch.testing.assert_close(got.float(), want.float(), rtol=1.6e-2, atol=1e-3)
+
+
+def test_segment_reference_case_table():
+    """The reference's CUDA segment test (tests/test_autotune.py:793-833), bit-exact."""
+    dev = _dev()
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        base = torch.full((1027, 2, 6), 0.1, dtype=dtype)
+        base[1, 0, 0] = float("inf")
+        base[2, 0, 0] = -float("inf")
+        base[3, 1, 2] = float("nan")
+        base[4, 1, 4] = -float("inf")
+        base_dev = base.to(dev)
+        for vi, view in enumerate((lambda b: b[:, :, ::2], lambda b: b.transpose(1, 2))):
+            data, data_dev = view(base), view(base_dev)
+            lengths = torch.tensor([0, 999, 2, 999, 1025, 999, 0, 999], dtype=torch.int32)[::2]
+            offsets = torch.tensor([1, 999, 1, 999, 3, 999, 1026, 999], dtype=torch.int64)[::2]
+            ldev = torch.tensor([0, 999, 2, 999, 1025, 999, 0, 999], dtype=torch.int32, device=dev)[::2]
+            odev = torch.tensor([1, 999, 1, 999, 3, 999, 1026, 999], dtype=torch.int64, device=dev)[::2]
+            for initial in (None, 0.0, -2.125):
+                for reduce in ("sum", "mean"):
+                    for seg, seg_dev, is_off in ((lengths, ldev, False), (offsets, odev, True)):
+                        _say(f"segment {dtype} view{vi} initial={initial} {reduce} offsets={is_off}")
+                        want = R.segment_reference(data, seg, reduce, offsets=is_off, initial=initial)
+                        got = CG.run_segment_pool(data_dev, seg_dev, reduce=reduce, initial=initial,
+                                                  offsets=is_off)
+                        _bits_equal(got.cpu(), want)
+            torch.testing.assert_close(data_dev.cpu(), data, rtol=0, atol=0, equal_nan=True)
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        data = torch.tensor([[1e-40, -0.0], [1e-40, 0.0]], dtype=dtype)
+        lengths = torch.tensor([0, 2])
+        for reduce in ("sum", "mean"):
+            _say(f"segment signed zero / denormal {dtype} {reduce}")
+            got = CG.run_segment_pool(data.to(dev), lengths.to(dev), reduce=reduce, initial=-0.0).cpu()
+            want = R.segment_reference(data, lengths, reduce, initial=-0.0)
+            _bits_equal(got, want)
+            assert torch.equal(torch.signbit(got), torch.signbit(want))
+    data = torch.zeros(1027, 3, dtype=torch.bfloat16)
+    lengths = torch.tensor([1027])
+    op = CG.as_segment_op("segment_mean", {"initial": 7.0}, lib="segment_gpu_tests")
+    _bits_equal(op(data.to(dev), lengths.to(dev)).cpu(),
+                R.segment_reference(data, lengths, "mean", initial=7.0))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_segment_cfg4_vector_path_bit_exact(dtype):
+    dev = _dev()
+    g = torch.Generator().manual_seed(4)
+    lengths = torch.poisson(torch.full((4096,), 20.0), generator=g).clamp(0, 200).to(torch.int32)
+    total = int(lengths.sum())
+    data = torch.randn(total, 128, generator=g).to(dtype)
+    offsets = torch.cat([torch.zeros(1, dtype=torch.int32), lengths.cumsum(0).to(torch.int32)])
+    for reduce in ("sum", "mean"):
+        _say(f"cfg4-style segment {dtype} {reduce} T={total}")
+        got = CG.run_segment_pool(data.to(dev), offsets.to(dev), reduce=reduce, offsets=True).cpu()
+        want = R.segment_reference(data, offsets, reduce, offsets=True)
+        _bits_equal(got, want)
