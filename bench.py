@@ -1,0 +1,280 @@
+"""Benchmark of the fused dependent-reduction folds on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-folds] [--no-cpu]
+
+Headline workload: the bf16 logsumexp / softmax-denominator fold
+over 16384 rows at widths {128, 1000, 4096, 32000} plus the split plan on 64 x 262144.
+One step = one pass of all five over their (resident, synthetic) inputs, replayed as a HIP
+graph.  `value` = algorithmic bytes of a step / step time (GB/s).  `roofline` is the dominant
+kernel (width 32000) timed with HIP events around a graph of back-to-back launches on its
+stream, its input larger than the 256 MB Infinity Cache (cold).  `per_fold` reports every
+configuration of BASELINE.json the same way (inputs rotated over > 512 MB so each launch is
+cold).  `cpu_baseline` times the oracle's eager CPU restatement on a bounded row sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for _p in (ROOT / "neptune-opt_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK = 8000.0            # GB/s, MI355X HBM3E
+BF16_PEAK = 2500.0           # TFLOP/s, MI355X dense bf16 MFMA
+METRIC = "achieved HBM GB/s (% of MI355X peak) per fused fold; attention TFLOP/s"
+COLD_BYTES = 768 << 20       # rotate inputs over more than the 256 MB Infinity Cache
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def seeded(seed):
+    import torch
+
+    return torch.Generator().manual_seed(seed)
+
+
+def graph_time(fn, replays: int, inner: int = 1, warmup: int = 2) -> float:
+    """Mean ms of one fn() call: fn is captured `inner` times into one HIP graph, replayed
+    `replays` times between events recorded on the replay stream."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warmup):
+            fn(0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(inner):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * inner)
+
+
+def copies_for(nbytes: int) -> int:
+    return max(1, math.ceil(COLD_BYTES / max(nbytes, 1)))
+
+
+# ---------------------------------------------------------------- workloads
+def cfg2_inputs(dev):
+    import torch
+
+    g = seeded(1)
+    xs = {}
+    for w in (128, 1000, 4096, 32000):
+        xs[w] = (4 * torch.randn(16384, w, generator=g)).bfloat16()
+    xs["split"] = (4 * torch.randn(64, 262144, generator=seeded(2))).bfloat16()
+    return xs, {k: v.to(dev) for k, v in xs.items()}
+
+
+def cfg2_bytes(w) -> int:
+    if w == "split":
+        return 64 * 262144 * 2 + 64 * 2
+    return 16384 * w * 2 + 16384 * 2
+
+
+def fold_gbs(nbytes, ms):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1e3, 2), "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK, 4)}
+
+
+def measure_fold(name, make, nbytes, rows, launches=20):
+    """Cold-cache kernel time of one fold: inputs rotated over > 512 MB inside one graph."""
+    n = copies_for(nbytes)
+    inputs = make(n)
+    inner = max(launches, n)
+    ms = graph_time(lambda i: inputs[i % n](), replays=5, inner=inner)
+    out = fold_gbs(nbytes, ms)
+    out["rows_per_s"] = round(rows / (ms * 1e-3), 1)
+    log(f"[bench] {name}: {out}")
+    return out
+
+
+def per_fold(dev, xs_dev):
+    import torch
+
+    import neptune_codegen as CG
+
+    folds = {}
+    # cfg1: fp32 logsumexp [8192, 1024], N(0, 3^2), seed 0
+    x1 = (3 * torch.randn(8192, 1024, generator=seeded(0))).to(dev)
+    b1 = 8192 * 1024 * 4 + 8192 * 4
+
+    def make1(n):
+        xs = [x1] + [x1.clone() for _ in range(n - 1)]
+        return [lambda x=x: CG.run("logsumexp", x) for x in xs]
+
+    folds["cfg1_logsumexp_f32_8192x1024"] = measure_fold("cfg1", make1, b1, 8192)
+    for w in (128, 1000, 4096, 32000, "split"):
+        x = xs_dev[w]
+
+        def make(n, x=x, w=w):
+            xs = [x] + [x.clone() for _ in range(n - 1)]
+            plan = "split" if w == "split" else "serial"
+            return [lambda y=y: CG.run("logsumexp", y, plan=plan) for y in xs]
+
+        rows = 64 if w == "split" else 16384
+        key = "cfg2_split_bf16_64x262144" if w == "split" else f"cfg2_logsumexp_bf16_16384x{w}"
+        folds[key] = measure_fold(key, make, cfg2_bytes(w), rows)
+    # cfg3: RMSNorm and L2-normalize bf16 [32768, 4096], seed 3
+    g3 = seeded(3)
+    x3 = torch.randn(32768, 4096, generator=g3).bfloat16().to(dev)
+    gamma = (1 + 0.1 * torch.randn(4096, generator=g3)).bfloat16().to(dev)
+    b3 = 2 * 32768 * 4096 * 2 + 4096 * 2
+
+    def make3(n, l2=False):
+        xs = [x3] + [x3.clone() for _ in range(n - 1)]
+        if l2:
+            return [lambda y=y: CG.run_l2_normalize(y, eps=1e-6) for y in xs]
+        return [lambda y=y: CG.run_rms_norm(y, gamma, eps=1e-6) for y in xs]
+
+    folds["cfg3_rms_norm_bf16_32768x4096"] = measure_fold("cfg3 rms", make3, b3, 32768)
+    folds["cfg3_l2_normalize_bf16_32768x4096"] = measure_fold("cfg3 l2", lambda n: make3(n, True), b3 - 8192, 32768)
+    del x3
+    # cfg4: fp16 CSR segment sum / mean, 65536 segments, Poisson(20) lengths in [0, 200]
+    g4 = seeded(4)
+    lengths = torch.poisson(torch.full((65536,), 20.0), generator=g4).clamp(0, 200).to(torch.int32)
+    total = int(lengths.sum())
+    data = torch.randn(total, 128, generator=g4).half().to(dev)
+    offsets = torch.cat([torch.zeros(1, dtype=torch.int32), lengths.cumsum(0).to(torch.int32)]).to(dev)
+    b4 = 256 * total + 4 * 65537 + 256 * 65536
+    for reduce in ("sum", "mean"):
+        def make4(n, reduce=reduce):
+            ds = [data] + [data.clone() for _ in range(n - 1)]
+            return [lambda d=d: CG.run_segment_pool(d, offsets, reduce=reduce, offsets=True) for d in ds]
+
+        folds[f"cfg4_segment_{reduce}_f16_65536x128"] = measure_fold(f"cfg4 {reduce}", make4, b4, 65536)
+    folds["cfg4_segment_tokens"] = total
+    del data
+    return folds
+
+
+def cpu_baseline(xs_cpu, seconds_target: float = 15.0):
+    """The oracle's eager restatement (torch.logsumexp(x.float()) on the host cores) over a
+    row sample of each cfg2 input; reported in GB/s of the same algorithmic bytes."""
+    import torch
+
+    from oracle import references as R
+
+    threads = torch.get_num_threads()
+    frac = 1 / 16
+    total_bytes, total_s = 0.0, 0.0
+    deadline = time.perf_counter() + seconds_target
+    reps = 0
+    while True:
+        for w, x in xs_cpu.items():
+            rows = max(1, int(x.shape[0] * frac))
+            sample = x[:rows]
+            t0 = time.perf_counter()
+            R.reference("logsumexp", sample)
+            total_s += time.perf_counter() - t0
+            total_bytes += cfg2_bytes(w) * rows / x.shape[0]
+        reps += 1
+        if time.perf_counter() > deadline or reps >= 8:
+            break
+    gbs = total_bytes / total_s / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"1/16 of the rows of each cfg2 input (widths 128/1000/4096/32000 and the "
+                      f"64x262144 split input), {reps} passes, {total_s:.1f} s of CPU work; "
+                      "oracle.references.reference('logsumexp') = torch.logsumexp(x.float(), -1)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-folds", action="store_true", help="skip the per-configuration table")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; every fold is row/segment-parallel and "
+              "shards without communication (see DESIGN.md), so only --gpus 1 is run.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import neptune_codegen as CG
+
+    dev = torch.device("cuda:0")
+    log(f"[bench] device {torch.cuda.get_device_name(dev)}, torch {torch.__version__}")
+    xs_cpu, xs = cfg2_inputs(dev)
+    widths = (128, 1000, 4096, 32000)
+
+    def step(_i=0):
+        for w in widths:
+            CG.run("logsumexp", xs[w])
+        CG.run("logsumexp", xs["split"], plan="split")
+
+    step_bytes = sum(cfg2_bytes(w) for w in widths) + cfg2_bytes("split")
+    # whole-job throughput: the step as one graph, W warmup + K timed replays
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(end) / args.steps
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"[bench] step {ms_step * 1e3:.1f} us, {value:.1f} GB/s")
+
+    # dominant kernel: width 32000 (1.05 GB per launch, larger than the Infinity Cache)
+    x32 = xs[32000]
+    dom_ms = graph_time(lambda i: CG.run("logsumexp", x32), replays=5, inner=20)
+    dom_bytes = cfg2_bytes(32000)
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                "kernel": "logsumexp_serial_bf16 (16384 x 32000)", "kernel_us": round(dom_ms * 1e3, 2),
+                "bytes_per_launch": dom_bytes}
+    log(f"[bench] dominant kernel {dom_ms * 1e3:.1f} us, {achieved:.1f} GB/s")
+    folds = None if args.no_folds else per_fold(dev, xs)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(xs_cpu)
+        log(f"[bench] cpu baseline {cpu}")
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (bf16 storage)",
+        "data": "synthetic: (4 * N(0,1)).bf16 from torch CPU generators, seed 1 (widths) and 2 (split)",
+        "config": {"workload": "cfg2 logsumexp fold, bf16, 16384 rows x width {128,1000,4096,32000} "
+                               "+ split plan 64 x 262144 (BLOCK 1024)",
+                   "frac_hbm_step": round(value / HBM_PEAK, 4), "step_bytes": step_bytes},
+        "roofline": roofline, "cpu_baseline": cpu, "per_fold": folds,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
