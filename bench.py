@@ -156,12 +156,23 @@ def per_fold(dev, xs_dev):
     data = torch.randn(total, 128, generator=g4).half().to(dev)
     offsets = torch.cat([torch.zeros(1, dtype=torch.int32), lengths.cumsum(0).to(torch.int32)]).to(dev)
     b4 = 256 * total + 4 * 65537 + 256 * 65536
+    from neptune_codegen.torch_op import compile_segment_reduction, launch_segment_kernel
+
+    out4 = torch.empty(65536, 128, dtype=torch.float16, device=dev)
     for reduce in ("sum", "mean"):
-        def make4(n, reduce=reduce):
+        program = compile_segment_reduction(f"segment_{reduce}", {"offsets": True})
+
+        def make4(n, reduce=reduce, program=program):
+            ds = [data] + [data.clone() for _ in range(n - 1)]
+            return [lambda d=d: launch_segment_kernel(program, d, offsets, out4) for d in ds]
+
+        def make4_op(n, reduce=reduce):
             ds = [data] + [data.clone() for _ in range(n - 1)]
             return [lambda d=d: CG.run_segment_pool(d, offsets, reduce=reduce, offsets=True) for d in ds]
 
-        folds[f"cfg4_segment_{reduce}_f16_65536x128"] = measure_fold(f"cfg4 {reduce}", make4, b4, 65536)
+        key = f"cfg4_segment_{reduce}_f16_65536x128"
+        folds[key] = measure_fold(f"cfg4 {reduce} kernel", make4, b4, 65536)
+        folds[key]["op_us_with_descriptor_asserts"] = measure_fold(f"cfg4 {reduce} op", make4_op, b4, 65536)["us"]
     folds["cfg4_segment_tokens"] = total
     del data
     return folds

@@ -276,6 +276,36 @@ __device__ __forceinline__ float finalize_state(const State& s, float n) {
 }
 
 // ---------------------------------------------------------------- fast exponential path
+// Raw slots of one tile: 16-byte words (VECTOR) or one element each (strided path).
+template <class St, int UNROLL, bool VECTOR>
+struct RawTile {
+  u32x4 w[VECTOR ? UNROLL : 1];
+  float s[VECTOR ? 1 : UNROLL];
+  bool ok[UNROLL];
+};
+
+template <class St, int TPR, int UNROLL, bool VECTOR>
+__device__ __forceinline__ void load_raw(RawTile<St, UNROLL, VECTOR>& r,
+                                         const typename St::T* row, i64 stride_col, i64 tile,
+                                         i64 c1, int t) {
+  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const i64 e = tile + (i64)(u * TPR + t) * TL::VEC;
+    r.ok[u] = e < c1;
+    if constexpr (VECTOR) {
+      if (r.ok[u]) r.w[u] = load16(row + e);
+    } else {
+      if (r.ok[u]) r.s[u] = St::load(row + e * stride_col);
+    }
+  }
+}
+
+// One lane's exponential fold over its slots of [c0, c1).  The next tile's loads are issued
+// before the current tile is folded, so each lane keeps up to 2*UNROLL loads in flight.
+// Per element: one max, one fma for the base-2 exponent, one exp2, one add.  The exponent
+// p*log2e - m*log2e carries an absolute error of about |m| * 2^-23, which is relative to the
+// readout m + log(acc): the row result keeps ~1e-7 relative accuracy.
 template <class F, class St, int TPR, int UNROLL, bool VECTOR>
 __device__ __forceinline__ LogLane log_row_lane(const typename St::T* row, i64 stride_col,
                                                 i64 c0, i64 c1, int t, float n) {
@@ -284,19 +314,24 @@ __device__ __forceinline__ LogLane log_row_lane(const typename St::T* row, i64 s
   s.m = -kInf;
   s.acc = 0.0f;
   s.flag = 0;
+  if (c0 >= c1) return s;
+  RawTile<St, UNROLL, VECTOR> cur;
+  load_raw<St, TPR, UNROLL, VECTOR>(cur, row, stride_col, c0, c1, t);
   for (i64 tile = c0; tile < c1; tile += TL::TILE) {
-    float v[TL::K];
-    bool ok[UNROLL];
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) ok[u] = TL::load_slot(row, stride_col, tile, c1, t, u, v);
+    RawTile<St, UNROLL, VECTOR> nxt;
+    const bool more = tile + TL::TILE < c1;
+    if (more) load_raw<St, TPR, UNROLL, VECTOR>(nxt, row, stride_col, tile + TL::TILE, c1, t);
     float p[TL::K];
     float tm = -kInf;
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
+      float v[TL::VEC];
+      if constexpr (VECTOR) St::unpack(cur.w[u], v);
+      else v[0] = cur.s[u];
 #pragma unroll
       for (int j = 0; j < TL::VEC; ++j) {
         const int k = u * TL::VEC + j;
-        p[k] = ok[u] ? F::phi(v[k], n) : -kInf;
+        p[k] = cur.ok[u] ? F::phi(v[j], n) : -kInf;
         tm = __builtin_fmaxf(tm, p[k]);
       }
     }
@@ -306,12 +341,16 @@ __device__ __forceinline__ LogLane log_row_lane(const typename St::T* row, i64 s
 #pragma unroll
       for (int k = 0; k < TL::K; ++k) s.flag |= is_nan(p[k]) ? 1 : 0;
     } else {
+      const float ml = mn * kLog2e;
+      // |m| above ~2.3e38 overflows m*log2e: route the row to the exact (subtracting) path.
+      if (!is_finite(ml) && is_finite(mn)) s.flag = 1;
       float a = s.acc * fast_exp(s.m - mn);
 #pragma unroll
-      for (int k = 0; k < TL::K; ++k) a += fast_exp(p[k] - mn);
+      for (int k = 0; k < TL::K; ++k) a += __builtin_amdgcn_exp2f(__builtin_fmaf(p[k], kLog2e, -ml));
       s.acc = a;
       s.m = mn;
     }
+    if (more) cur = nxt;
   }
   return s;
 }

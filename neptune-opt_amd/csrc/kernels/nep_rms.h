@@ -86,7 +86,9 @@ __device__ __forceinline__ float rms_scale(float total, float count, float eps) 
 }
 
 // Serial plan: x [rows, ncols] strided -> out [rows, ncols] contiguous.
-// Requires ncols <= TPR * NV * VEC (checked by the host).
+// Requires ncols <= TPR * NV * VEC (checked by the host).  The vector path keeps the row and
+// gamma as packed 16-byte words (NV words each per lane) and unpacks on use, which halves the
+// registers of holding them as fp32.
 template <class St, int TPR, int NV, bool VECTOR, bool L2, int WG>
 __device__ __forceinline__ void rms_serial(const typename St::T* __restrict__ x,
                                            const typename St::T* __restrict__ gamma,
@@ -98,34 +100,75 @@ __device__ __forceinline__ void rms_serial(const typename St::T* __restrict__ x,
   constexpr int RPW = WG / TPR;
   __shared__ float lds[WG / 64];
   const int t = threadIdx.x % TPR;
-  float g[NV * VEC];
-  if constexpr (!L2) {
-#pragma unroll
-    for (int u = 0; u < NV; ++u)
-      IO::load_gamma(gamma, stride_gamma, (i64)(u * TPR + t) * VEC, ncols, g + u * VEC);
-  }
   const float count = (float)ncols;
-  for (i64 base = (i64)blockIdx.x * RPW; base < rows; base += (i64)gridDim.x * RPW) {
-    const i64 row = base + threadIdx.x / TPR;
-    const bool live = row < rows;
-    const i64 c1 = live ? ncols : 0;
-    const typename St::T* rp = x + (live ? row : 0) * stride_row;
-    float v[NV * VEC];
+  if constexpr (VECTOR) {
+    u32x4 graw[L2 ? 1 : NV];
+    if constexpr (!L2) {
 #pragma unroll
-    for (int u = 0; u < NV; ++u) IO::load(rp, stride_col, (i64)(u * TPR + t) * VEC, c1, v + u * VEC);
-    float total = 0.0f;
+      for (int u = 0; u < NV; ++u) {
+        const i64 e = (i64)(u * TPR + t) * VEC;
+        graw[u] = e < ncols ? load16_cached(gamma + e) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    for (i64 base = (i64)blockIdx.x * RPW; base < rows; base += (i64)gridDim.x * RPW) {
+      const i64 row = base + threadIdx.x / TPR;
+      const bool live = row < rows;
+      const i64 c1 = live ? ncols : 0;
+      const typename St::T* rp = x + (live ? row : 0) * stride_row;
+      u32x4 xr[NV];
 #pragma unroll
-    for (int k = 0; k < NV * VEC; ++k) total += v[k] * v[k];
-    total = row_sum<TPR>(total, lds);
-    const float scale = rms_scale<L2>(total, count, eps);
-    typename St::T* op = out + (live ? row : 0) * ncols;
+      for (int u = 0; u < NV; ++u) {
+        const i64 e = (i64)(u * TPR + t) * VEC;
+        xr[u] = e < c1 ? load16(rp + e) : u32x4{0u, 0u, 0u, 0u};
+      }
+      float total = 0.0f;
 #pragma unroll
-    for (int u = 0; u < NV; ++u) {
-      float y[VEC];
+      for (int u = 0; u < NV; ++u) {
+        float v[VEC];
+        St::unpack(xr[u], v);
 #pragma unroll
-      for (int j = 0; j < VEC; ++j)
-        y[j] = rms_readout<St, L2>(v[u * VEC + j], L2 ? 0.0f : g[u * VEC + j], scale);
-      IO::store(op, (i64)(u * TPR + t) * VEC, c1, y);
+        for (int j = 0; j < VEC; ++j) total += v[j] * v[j];
+      }
+      total = row_sum<TPR>(total, lds);
+      const float scale = rms_scale<L2>(total, count, eps);
+      typename St::T* op = out + (live ? row : 0) * ncols;
+#pragma unroll
+      for (int u = 0; u < NV; ++u) {
+        const i64 e = (i64)(u * TPR + t) * VEC;
+        if (e >= c1) continue;
+        float v[VEC], g[VEC], y[VEC];
+        St::unpack(xr[u], v);
+        if constexpr (!L2) St::unpack(graw[u], g);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) y[j] = rms_readout<St, L2>(v[j], L2 ? 0.0f : g[j], scale);
+        store16(op + e, St::pack(y));
+      }
+    }
+  } else {
+    float g[L2 ? 1 : NV];
+    if constexpr (!L2) {
+#pragma unroll
+      for (int u = 0; u < NV; ++u) IO::load_gamma(gamma, stride_gamma, (i64)(u * TPR + t), ncols, g + u);
+    }
+    for (i64 base = (i64)blockIdx.x * RPW; base < rows; base += (i64)gridDim.x * RPW) {
+      const i64 row = base + threadIdx.x / TPR;
+      const bool live = row < rows;
+      const i64 c1 = live ? ncols : 0;
+      const typename St::T* rp = x + (live ? row : 0) * stride_row;
+      float v[NV];
+#pragma unroll
+      for (int u = 0; u < NV; ++u) IO::load(rp, stride_col, (i64)(u * TPR + t), c1, v + u);
+      float total = 0.0f;
+#pragma unroll
+      for (int u = 0; u < NV; ++u) total += v[u] * v[u];
+      total = row_sum<TPR>(total, lds);
+      const float scale = rms_scale<L2>(total, count, eps);
+      typename St::T* op = out + (live ? row : 0) * ncols;
+#pragma unroll
+      for (int u = 0; u < NV; ++u) {
+        float y = rms_readout<St, L2>(v[u], L2 ? 0.0f : g[u], scale);
+        IO::store(op, (i64)(u * TPR + t), c1, &y);
+      }
     }
   }
 }

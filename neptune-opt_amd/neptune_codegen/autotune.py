@@ -63,7 +63,12 @@ def device_name_of(device) -> str | None:
         device = torch.device(device)
         if device.type != "cuda":
             return None
-        return torch.cuda.get_device_name(device)
+        name = torch.cuda.get_device_name(device)
+        # ROCm builds without the marketing-name table report a generic name; the ISA then
+        # identifies the part (gfx950 = MI350X/MI355X) and keys its launch table.
+        if not name or "Radeon Graphics" in name:
+            name = torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]
+        return name
     except Exception:  # noqa: BLE001
         return None
 

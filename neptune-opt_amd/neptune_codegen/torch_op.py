@@ -337,19 +337,27 @@ def _launch_segment(name, data, segments, params, plan, *, wrapper=None):
     if (type(shape[0]) is int and shape[0] == 0) or (type(channels) is int and channels == 0):
         return out
     flat = data.reshape(data.shape[0], channels)
-    program = compile_segment_reduction(name, params, plan)
+    launch_segment_kernel(compile_segment_reduction(name, params, plan), flat, spans, out)
+    return out
+
+
+def launch_segment_kernel(program, flat, spans, out):
+    """The fold launch alone: flat [nrows, channels] data, validated spans [nsegments + 1],
+    out [nsegments, channels] (contiguous).  Callers own the span checks."""
+    import torch
+
+    channels = flat.shape[1]
+    nseg = spans.shape[0] - 1
     var = _segment_variant(flat, spans, channels)
-    device = data.device.index if data.device.index is not None else torch.cuda.current_device()
+    device = flat.device.index if flat.device.index is not None else torch.cuda.current_device()
     kernel = program.kernel(var, device)
-    nseg = shape[0]
     if var.vector:
         grid = (max(1, -(-nseg // (256 // var.lps))),)
     else:
         grid = (nseg, -(-channels // 64))
-    kernel.launch(grid, (flat.data_ptr(), spans.data_ptr(), out.data_ptr(), data.shape[0], channels,
-                         nseg, flat.stride(0), flat.stride(1), spans.stride(0)),
-                  hip.current_stream(data.device))
-    return out
+    kernel.launch(grid, (flat.data_ptr(), spans.data_ptr(), out.data_ptr(), flat.shape[0],
+                         channels, nseg, flat.stride(0), flat.stride(1), spans.stride(0)),
+                  hip.current_stream(flat.device))
 
 
 def run_segment_pool(data, segments, *, reduce="sum", offsets=False, initial=None,
