@@ -175,6 +175,17 @@ def per_fold(dev, xs_dev):
         folds[key]["op_us_with_descriptor_asserts"] = measure_fold(f"cfg4 {reduce} op", make4_op, b4, 65536)["us"]
     folds["cfg4_segment_tokens"] = total
     del data
+    # cfg5: causal attention fold, B=4 H=32 S=4096 D=128 bf16, seed 5
+    g5 = seeded(5)
+    shape = (4, 32, 4096, 128)
+    q, k, v = ((torch.randn(*shape, generator=g5).bfloat16()).to(dev) for _ in range(3))
+    ms = graph_time(lambda i: CG.run_attention(q, k, v, causal=True), replays=3, inner=4)
+    flops = 4 * 4 * 32 * 128 * 4096 * 4097 // 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    folds["cfg5_attention_causal_bf16_4x32x4096x128"] = {
+        "us": round(ms * 1e3, 1), "TFLOP_s": round(tflops, 1), "frac_mfma_bf16": round(tflops / BF16_PEAK, 4),
+        "flops": flops, "query_rows_per_s": round(4 * 32 * 4096 / (ms * 1e-3), 1)}
+    log(f"[bench] cfg5 attention: {folds['cfg5_attention_causal_bf16_4x32x4096x128']}")
     return folds
 
 

@@ -1,0 +1,127 @@
+"""Online-softmax attention fold: O = softmax(scale * Q K^T [+ causal mask]) V.
+
+There is no reference function for this path (attention-chain fusion is a non-goal of the
+reference, docs/roadmap.md:28-30); the fold is the logsumexp skeleton's repair
+exp(s - s2) (tests/test_neptune_opt.py:347) applied per key tile to the running
+(max, sum, output) state, with MFMA for Q K^T and P V.  The causal mask is torch's
+`is_causal=True` (query i sees keys j <= i).  The oracle is the closed form in fp32.
+
+Layout contract: q [B, H, Sq, D], k/v [B, H, Sk, D], bf16, unit stride on D; other strides
+are honoured (rows must be 16-byte aligned, otherwise the input is made contiguous).  Output
+is a fresh contiguous [B, H, Sq, D] bf16 tensor; `return_lse` adds the fp32 [B, H, Sq]
+natural-log logsumexp of the scaled, masked scores.
+"""
+from __future__ import annotations
+
+import math
+import threading
+
+from neptune_codegen import hip
+from neptune_codegen.emitters import BASE_OPTIONS, attention_kernel_name, emit_attention_source
+
+_PROGRAMS: dict = {}
+_OPS: dict = {}
+_lock = threading.Lock()
+LOG2E = 1.4426950408889634
+BLOCK_M = 128
+
+
+def _program(head_dim: int, causal: bool) -> hip.Program:
+    key = (head_dim, causal)
+    with _lock:
+        prog = _PROGRAMS.get(key)
+        if prog is None:
+            prog = hip.Program(emit_attention_source(head_dim, causal),
+                               f"{attention_kernel_name(head_dim, causal)}.hip", BASE_OPTIONS)
+            _PROGRAMS[key] = prog
+        return prog
+
+
+def validate_attention_inputs(q, k, v, *, metadata: bool = False):
+    import torch
+
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+        if t.layout != torch.strided:
+            raise TypeError(f"attention {nm} must be strided")
+        if t.ndim != 4:
+            raise ValueError(f"attention {nm} must be [batch, heads, seq, head_dim]")
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"attention fold supports bfloat16 inputs, got {t.dtype} for {nm}")
+        if not metadata and t.device.type != "cuda":
+            raise ValueError("attention execution requires a ROCm (cuda) device")
+    if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"attention shapes do not match: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("attention tensors must be on the same device")
+    if q.shape[3] not in (64, 128):
+        raise NotImplementedError("attention fold supports head_dim 64 and 128")
+    if k.shape[2] == 0:
+        raise ValueError("attention needs at least one key")
+    return tuple(q.shape)
+
+
+def _kernel_ready(t):
+    ok = (t.stride(3) == 1 and all(s % 8 == 0 for s in t.stride()[:3]) and t.data_ptr() % 16 == 0)
+    return t if ok else t.contiguous()
+
+
+def run_attention(q, k, v, *, scale: float | None = None, causal: bool = True,
+                  return_lse: bool = False):
+    """Attention fold on the current stream; see the module docstring for the contract."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensor
+
+    metadata = isinstance(q, FakeTensor) or q.device.type == "meta"
+    shape = validate_attention_inputs(q, k, v, metadata=metadata)
+    B, H, Sq, D = shape
+    out = torch.empty(shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device) if return_lse else None
+    if metadata or out.numel() == 0:
+        return (out, lse) if return_lse else out
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    if not math.isfinite(scale) or scale <= 0:
+        raise ValueError("attention scale must be finite and positive")
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    device = q.device.index if q.device.index is not None else torch.cuda.current_device()
+    kernel = _program(D, causal).kernel(
+        attention_kernel_name(D, causal),
+        (hip.PTR,) * 5 + (hip.I32,) * 3 + (hip.I64,) * 9 + (hip.F32,), 256, device)
+    nqb = (Sq + BLOCK_M - 1) // BLOCK_M
+    kernel.launch((nqb * B * H,),
+                  (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                   lse.data_ptr() if lse is not None else 0, H, Sq, k.shape[2],
+                   q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+                   v.stride(0), v.stride(1), v.stride(2), scale * LOG2E),
+                  hip.current_stream(q.device))
+    return (out, lse) if return_lse else out
+
+
+attention_fold = run_attention
+
+
+def as_attention_op(scale: float | None = None, causal: bool = True, lib: str = "neptune"):
+    """Custom op `(Tensor q, Tensor k, Tensor v) -> Tensor` with scale and mask in its name."""
+    import torch
+
+    from neptune_codegen.autotune import parameter_tag
+
+    params = {"scale": float(scale)} if scale is not None else {}
+    key = (lib, tuple(sorted(params.items())), causal)
+    with _lock:
+        if key in _OPS:
+            return _OPS[key]
+    name = f"attention_fold{parameter_tag(params)}_{'causal' if causal else 'full'}"
+
+    def _impl(q, k, v):
+        return run_attention(q, k, v, scale=scale, causal=causal)
+
+    def _fake(q, k, v):
+        validate_attention_inputs(q, k, v, metadata=True)
+        return torch.empty(q.shape, dtype=q.dtype, device=q.device)
+
+    op = torch.library.custom_op(f"{lib}::{name}", mutates_args=(),
+                                 schema="(Tensor q, Tensor k, Tensor v) -> Tensor")(_impl)
+    op.register_fake(_fake)
+    with _lock:
+        _OPS[key] = op
+    return op

@@ -451,3 +451,28 @@ def emit_segment_source(name: str, *, initial=None, offsets=False, plan="serial"
 
 def segment_kernel_name(name: str, var: SegmentVariant) -> str:
     return f"{name}_{var.tag()}"
+
+
+# ---------------------------------------------------------------- attention fold
+def emit_attention_source(head_dim: int, causal: bool) -> str:
+    """hiprtc unit of the online-softmax attention fold (no reference counterpart): the
+    logsumexp repair exp(s - s2) applied per key tile to (m, l, O)."""
+    if head_dim not in (64, 128):
+        raise NotImplementedError("attention fold supports head_dim 64 and 128")
+    name = attention_kernel_name(head_dim, causal)
+    return "\n".join([
+        "// AUTO-GENERATED by neptune_codegen (HIP emitter) -- do not edit.\n"
+        f"// online-softmax attention fold: head_dim={head_dim}, causal={causal}; bf16 MFMA, fp32 "
+        "running max/sum.\n",
+        kernel_header("nep_device.h", "nep_attention.h"),
+        f'extern "C" __global__ void __launch_bounds__(256) {name}(const void* q, const void* k, '
+        "const void* v, void* o, float* lse, int heads, int sq, int sk, long long qsb, long long qsh, "
+        "long long qss, long long ksb, long long ksh, long long kss, long long vsb, long long vsh, "
+        "long long vss, float scale_log2) {\n"
+        f"  nep::attention_fwd<{head_dim}, {'true' if causal else 'false'}>((const __bf16*)q, "
+        "(const __bf16*)k, (const __bf16*)v, (__bf16*)o, lse, heads, sq, sk, qsb, qsh, qss, ksb, ksh, "
+        "kss, vsb, vsh, vss, scale_log2);\n}\n"])
+
+
+def attention_kernel_name(head_dim: int, causal: bool) -> str:
+    return f"attention_fold_d{head_dim}_{'causal' if causal else 'full'}"

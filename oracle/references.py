@@ -103,7 +103,7 @@ def attention_reference(q, k, v, *, scale=None, causal=True):
     s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * scale
     if causal:
         n, m = s.shape[-2], s.shape[-1]
-        mask = torch.ones(n, m, dtype=torch.bool).tril(diagonal=m - n)
+        mask = torch.ones(n, m, dtype=torch.bool).tril(diagonal=0)  # torch is_causal: j <= i
         s = s.masked_fill(~mask, float("-inf"))
     p = torch.softmax(s, dim=-1)
     return torch.matmul(p, vf).to(q.dtype)

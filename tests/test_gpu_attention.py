@@ -1,0 +1,113 @@
+"""GPU parity of the online-softmax attention fold against the fp32 closed form.
+
+Tolerance: bf16 rtol 1.6e-2 / atol 1e-3, against
+softmax(scale * Q K^T + torch is_causal mask) V computed in fp32 on the CPU.
+"""
+import math
+
+import pytest
+import torch
+
+import neptune_codegen as CG
+from neptune_codegen import hip
+from neptune_codegen.emitters import BASE_OPTIONS, kernel_header
+from oracle import references as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a ROCm GPU")
+    return torch.device("cuda:0")
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def test_mfma_32x32x16_bf16_accumulator_layout():
+    """The kernel relies on: A lane l holds row l%32 with k = 8*(l/32)+i; B lane l holds column
+    l%32 with the same k; accumulator register r of lane l is C[8*(r/4) + 4*(l/32) + r%4][l%32]."""
+    dev = _dev()
+    src = kernel_header("nep_device.h", "nep_attention.h") + r'''
+extern "C" __global__ void mfma_probe(const __bf16* a, const __bf16* b, float* c) {
+  const int l = threadIdx.x, m = l & 31, hi = l >> 5;
+  nep::bf16x8 av, bv;
+  for (int i = 0; i < 8; ++i) {
+    av[i] = a[m * 16 + 8 * hi + i];        // A is 32 x 16, row-major
+    bv[i] = b[(8 * hi + i) * 32 + m];      // B is 16 x 32, row-major
+  }
+  nep::f32x16 acc = {};
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+  for (int r = 0; r < 16; ++r) c[(8 * (r / 4) + 4 * hi + (r % 4)) * 32 + m] = acc[r];
+}
+'''
+    prog = hip.Program(src, "mfma_probe.hip", BASE_OPTIONS)
+    k = prog.kernel("mfma_probe", (hip.PTR,) * 3, 64, 0)
+    g = torch.Generator().manual_seed(11)
+    a = torch.randint(-4, 5, (32, 16), generator=g).to(torch.bfloat16)
+    b = torch.randint(-4, 5, (16, 32), generator=g).to(torch.bfloat16)
+    c = torch.empty(32, 32, device=dev)
+    ad, bd = a.to(dev), b.to(dev)
+    k.launch((1,), (ad.data_ptr(), bd.data_ptr(), c.data_ptr()), hip.current_stream(dev))
+    torch.testing.assert_close(c.cpu(), a.float() @ b.float(), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(1, 2, 256, 256, 128), (2, 3, 200, 200, 128), (1, 1, 77, 77, 128),
+                                   (1, 2, 130, 333, 64), (1, 1, 1, 64, 128), (1, 4, 512, 512, 64)])
+def test_attention_parity(shape, causal):
+    dev = _dev()
+    B, H, Sq, Sk, D = shape
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(B, H, Sq, D, generator=g).bfloat16()
+    k = torch.randn(B, H, Sk, D, generator=g).bfloat16()
+    v = torch.randn(B, H, Sk, D, generator=g).bfloat16()
+    _say(f"attention {shape} causal={causal}")
+    got, lse = CG.run_attention(q.to(dev), k.to(dev), v.to(dev), causal=causal, return_lse=True)
+    want = R.attention_reference(q, k, v, causal=causal)
+    torch.testing.assert_close(got.cpu().float(), want.float(), rtol=1.6e-2, atol=1e-3)
+    s = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) / math.sqrt(D)
+    if causal:
+        s = s.masked_fill(~torch.ones(Sq, Sk, dtype=torch.bool).tril(0), float("-inf"))
+    torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=1e-4, atol=1e-4)
+
+
+def test_attention_strided_layout_and_scale():
+    """[B, S, H, D] storage viewed as [B, H, S, D] (the common projection layout)."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(6)
+    qs = torch.randn(2, 300, 4, 128, generator=g).bfloat16()
+    ks = torch.randn(2, 300, 4, 128, generator=g).bfloat16()
+    vs = torch.randn(2, 300, 4, 128, generator=g).bfloat16()
+    q, k, v = (t.transpose(1, 2) for t in (qs, ks, vs))
+    _say("attention strided [B,S,H,D] view, scale 0.05")
+    got = CG.run_attention(qs.to(dev).transpose(1, 2), ks.to(dev).transpose(1, 2),
+                           vs.to(dev).transpose(1, 2), scale=0.05, causal=True)
+    want = R.attention_reference(q, k, v, scale=0.05, causal=True)
+    torch.testing.assert_close(got.cpu().float(), want.float(), rtol=1.6e-2, atol=1e-3)
+
+
+def test_attention_cfg5_shape_head_subset():
+    """cfg5 (B=4, H=32, S=4096, D=128, causal) on the GPU; two heads checked on the CPU."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(5)
+    shape = (4, 32, 4096, 128)
+    q, k, v = (torch.randn(*shape, generator=g).bfloat16() for _ in range(3))
+    _say("attention cfg5 [4,32,4096,128] causal")
+    got = CG.run_attention(q.to(dev), k.to(dev), v.to(dev), causal=True).cpu()
+    for b, h in ((0, 0), (3, 31)):
+        want = R.attention_reference(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1])
+        torch.testing.assert_close(got[b:b + 1, h:h + 1].float(), want.float(), rtol=1.6e-2, atol=1e-3)
+    assert torch.isfinite(got.float()).all()
+
+
+def test_attention_custom_op():
+    dev = _dev()
+    op = CG.as_attention_op(causal=True)
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(1, 2, 64, 64, generator=g).bfloat16() for _ in range(3))
+    got = op(q.to(dev), k.to(dev), v.to(dev))
+    torch.testing.assert_close(got.cpu().float(), R.attention_reference(q, k, v).float(),
+                               rtol=1.6e-2, atol=1e-3)
