@@ -10,13 +10,16 @@
 //    dims per lane from LDS), B = Q^T (query = lane%32, 8 head dims, held in registers).  The
 //    32x32 result gives lane l the scores of query l%32 for keys 8*(r/4) + 4*(l/32) + r%4, so
 //    the softmax of a query needs its own 32 registers plus one exchange with lane l^32.
-//  * O^T += V^T P^T: B = P^T straight from the score registers (bf16), A = V^T read from an LDS
-//    copy of the tile stored transposed ([dim][key]).  The MFMA contraction order over keys is
+//  * O^T += V^T P^T: B = P^T straight from the score registers, A = V^T read from an LDS copy
+//    of the tile stored transposed ([dim][key]).  The MFMA contraction order over keys is
 //    permuted identically in A and B, which is what lets P^T stay in its accumulator layout.
-//  * P V runs in fp16 (unit roundoff 2^-11, 8x finer than bf16 for P in (0, 1]): V is
-//    converted bf16 -> fp16 while it is staged, which is exact for |v| in fp16's normal range.
-//    A key tile holding any |v| > 65504 is staged and multiplied in bf16 instead (a
-//    workgroup-uniform decision taken at the staging barrier).
+//  * P V runs in fp16 (unit roundoff 2^-11, 8x finer than bf16 for P): V is converted
+//    bf16 -> fp16 while staged, exact for |v| < 65536.  If any staged V tile of a query block
+//    holds a larger magnitude, the block is recomputed with P V in bf16 (a second instance of
+//    the loop, so the two modes do not add up in registers).
+//  * Lazy rescaling: the reference max only moves when the running max exceeds it by more than
+//    8 (base 2), so P <= 256 (exact range of fp16) and O is rescaled on few tiles.
+//  * The row sum l accumulates the fp16-rounded P with v_dot2 (the values the MFMA multiplies).
 //  * Tiles above the causal diagonal are skipped per wave; workgroups run heaviest query block
 //    first and a head's blocks share one XCD (workgroup id % 8 == head % 8), so its K/V stay in
 //    that XCD's L2.
@@ -35,13 +38,14 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 constexpr int kAttnBM = 128;           // queries per workgroup
 constexpr int kAttnBN = 64;            // keys per tile
 constexpr int kAttnWaves = 4;
+constexpr float kRescaleSlack = 8.0f;  // base-2 headroom before the reference max moves
 
 template <int D>
 struct AttnLds {
   static constexpr int KSTRIDE = D + 8;         // bf16 per K row (16-byte pad)
-  static constexpr int VSTRIDE = kAttnBN + 4;   // bf16 per V^T row (8-byte pad)
+  static constexpr int VSTRIDE = kAttnBN + 4;   // 16-bit words per V^T row (8-byte pad)
   __bf16 k[kAttnBN * KSTRIDE];
-  __bf16 vt[D * VSTRIDE];
+  u16 vt[D * VSTRIDE];
 };
 
 __device__ __forceinline__ u32 pack_bf16x2(float a, float b) {
@@ -55,6 +59,216 @@ __device__ __forceinline__ u32 pack_f16x2(float a, float b) {
   return half2_bits(h);
 }
 
+// Per-query-block state and the key-tile loop, in one P V precision.
+template <int D, bool CAUSAL, bool F16V>
+struct AttnBlock {
+  static constexpr int KSTEPS = D / 16;          // MFMA k-steps of S^T
+  static constexpr int DBLK = D / 32;            // 32-row blocks of O^T
+  static constexpr int CHUNKS = D / 8;           // 16-byte chunks per row
+  static constexpr int NT = 64 * kAttnWaves;
+  static constexpr int KITEMS = kAttnBN * CHUNKS;           // 16-byte K pieces per tile
+  static constexpr int VITEMS = (kAttnBN / 4) * CHUNKS;     // (key quad, dim chunk) V pieces
+  static constexpr int KLOADS = (KITEMS + NT - 1) / NT;
+  static constexpr int VLOADS = (VITEMS + NT - 1) / NT;
+
+  // Runs the block; returns false (after a uniform early exit) if F16V meets an fp16 overflow.
+  __device__ static bool run(AttnLds<D>& sm, const bf16x8* qreg, const __bf16* kp,
+                             const __bf16* vp, i64 kss, i64 vss, int sk, int q0, int qw,
+                             int my_q, float c, f32x16* oacc, float& m_out, float& l_out) {
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+    int kv_end = sk;
+    if constexpr (CAUSAL) kv_end = min(sk, q0 + kAttnBM);
+    const int ntiles = (kv_end + kAttnBN - 1) / kAttnBN;
+#pragma unroll
+    for (int a = 0; a < DBLK; ++a) oacc[a] = f32x16{};
+    float m_ref = -kInf;   // reference max (base 2) of this lane's query
+    float l_run = 0.0f;
+
+    u32x4 kbuf[KLOADS];
+    u32x4 vbuf[VLOADS][4];
+    auto fetch = [&](int tile) {
+      const int k0 = tile * kAttnBN;
+#pragma unroll
+      for (int i = 0; i < KLOADS; ++i) {
+        const int cc = tid + i * NT;
+        const int key = k0 + cc / CHUNKS, ch = cc % CHUNKS;
+        kbuf[i] = (cc < KITEMS && key < sk) ? load16_cached(kp + (i64)key * kss + ch * 8)
+                                            : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int i = 0; i < VLOADS; ++i) {
+        const int cc = tid + i * NT;
+        const int ch = cc % CHUNKS, quad = cc / CHUNKS;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + quad * 4 + r;
+          vbuf[i][r] = (cc < VITEMS && key < sk) ? load16_cached(vp + (i64)key * vss + ch * 8)
+                                                 : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    };
+    // any |v| >= 65536 (bf16 magnitude bits >= 0x4780) does not fit fp16
+    auto overflow = [&]() -> int {
+      u32 mx = 0;
+#pragma unroll
+      for (int i = 0; i < VLOADS; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const u32 x = vbuf[i][r][w] & 0x7fff7fffu;
+            mx = max(mx, max(x & 0xffffu, x >> 16));
+          }
+      return mx >= 0x4780u ? 1 : 0;
+    };
+    auto stash = [&]() {
+#pragma unroll
+      for (int i = 0; i < KLOADS; ++i) {
+        const int cc = tid + i * NT;
+        const int key = cc / CHUNKS, ch = cc % CHUNKS;
+        if (cc < KITEMS) *(u32x4*)(sm.k + key * AttnLds<D>::KSTRIDE + ch * 8) = kbuf[i];
+      }
+#pragma unroll
+      for (int i = 0; i < VLOADS; ++i) {
+        const int cc = tid + i * NT;
+        if (cc >= VITEMS) continue;
+        const int ch = cc % CHUNKS, quad = cc / CHUNKS;
+        // head dim ch*8 + j of the 4 keys of the quad -> V^T[dim][quad*4 .. +3]
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int word = j >> 1;
+          u32 e[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) e[r] = vbuf[i][r][word];
+          u32x2 w;
+          if constexpr (F16V) {
+            // bf16 -> fp32 is a shift / mask; two fp32 -> one packed fp16 pair (exact here)
+            if (j & 1) {
+              w.x = pack_f16x2(as_f32(e[0] & 0xffff0000u), as_f32(e[1] & 0xffff0000u));
+              w.y = pack_f16x2(as_f32(e[2] & 0xffff0000u), as_f32(e[3] & 0xffff0000u));
+            } else {
+              w.x = pack_f16x2(as_f32(e[0] << 16), as_f32(e[1] << 16));
+              w.y = pack_f16x2(as_f32(e[2] << 16), as_f32(e[3] << 16));
+            }
+          } else {
+            if (j & 1) {
+              w.x = (e[0] >> 16) | (e[1] & 0xffff0000u);
+              w.y = (e[2] >> 16) | (e[3] & 0xffff0000u);
+            } else {
+              w.x = (e[0] & 0xffffu) | (e[1] << 16);
+              w.y = (e[2] & 0xffffu) | (e[3] << 16);
+            }
+          }
+          *(u32x2*)(sm.vt + (ch * 8 + j) * AttnLds<D>::VSTRIDE + quad * 4) = w;
+        }
+      }
+    };
+
+    if (ntiles > 0) fetch(0);
+    for (int tile = 0; tile < ntiles; ++tile) {
+      // barrier: every wave is done with the previous tile in LDS (and, in fp16 mode, the
+      // workgroup agrees on whether this V tile fits fp16)
+      if constexpr (F16V) {
+        if (__syncthreads_or(overflow())) return false;
+      } else {
+        __syncthreads();
+      }
+      stash();
+      __syncthreads();
+      if (tile + 1 < ntiles) fetch(tile + 1);
+      const int k0 = tile * kAttnBN;
+      if (CAUSAL && k0 > qw + 31) continue;   // tile entirely above this wave's diagonal
+      // ---- S^T = K Q^T for the two 32-key blocks of the tile
+      f32x16 sacc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        sacc[kb] = f32x16{};
+        const __bf16* krow = sm.k + (kb * 32 + l32) * AttnLds<D>::KSTRIDE + 8 * hi;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+          const bf16x8 a = *(const bf16x8*)(krow + 16 * s);
+          sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[kb], 0, 0, 0);
+        }
+      }
+      // ---- masks only on the diagonal tile and the ragged last tile
+      const bool need_mask = (CAUSAL && k0 + kAttnBN - 1 > qw) || (k0 + kAttnBN > sk);
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+            if ((CAUSAL && key > my_q) || key >= sk) sacc[kb][r] = -kInf;
+          }
+      }
+      float tmax = -kInf;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tmax = __builtin_fmaxf(tmax, sacc[kb][r]);
+      tmax = __builtin_fmaxf(tmax, partner<32>(tmax)) * c;
+      // move the reference max only when P would exceed 2^8 (or on the first finite tile)
+      const bool move = tmax > m_ref + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(move) != 0) {
+        const float m_new = move ? tmax : m_ref;
+        const float alpha = (m_ref == -kInf) ? 0.0f : __builtin_amdgcn_exp2f(m_ref - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int a = 0; a < DBLK; ++a) oacc[a] *= alpha;
+        m_ref = m_new;
+      }
+      const float shift = (m_ref == -kInf) ? 0.0f : m_ref;
+      u32 pk[2][8];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r], c, -shift));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r + 1], c, -shift));
+          if constexpr (F16V) {
+            const u32 w = pack_f16x2(p0, p1);
+            pk[kb][r >> 1] = w;
+            l_run = __builtin_amdgcn_fdot2(as_half2(w), half2_t{(_Float16)1.0f, (_Float16)1.0f},
+                                           l_run, false);
+          } else {
+            pk[kb][r >> 1] = pack_bf16x2(p0, p1);
+            l_run += p0 + p1;
+          }
+        }
+      // ---- O^T += V^T P^T over the 4 key steps (16 keys each) of the tile
+#pragma unroll
+      for (int cs = 0; cs < 4; ++cs) {
+        const int kb = cs >> 1, half = cs & 1;
+        u32x4 bw;
+        bw.x = pk[kb][4 * half + 0];
+        bw.y = pk[kb][4 * half + 1];
+        bw.z = pk[kb][4 * half + 2];
+        bw.w = pk[kb][4 * half + 3];
+        const int kbase = kb * 32 + 16 * half + 4 * hi;
+#pragma unroll
+        for (int a = 0; a < DBLK; ++a) {
+          const u16* vrow = sm.vt + (a * 32 + l32) * AttnLds<D>::VSTRIDE + kbase;
+          const u32x2 lo = *(const u32x2*)(vrow);
+          const u32x2 up = *(const u32x2*)(vrow + 8);
+          const u32x4 av = {lo.x, lo.y, up.x, up.y};
+          if constexpr (F16V) {
+            oacc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, av),
+                                                             __builtin_bit_cast(f16x8, bw),
+                                                             oacc[a], 0, 0, 0);
+          } else {
+            oacc[a] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av),
+                                                              __builtin_bit_cast(bf16x8, bw),
+                                                              oacc[a], 0, 0, 0);
+          }
+        }
+      }
+    }
+    m_out = m_ref;
+    l_out = l_run;
+    return true;
+  }
+};
+
 template <int D, bool CAUSAL>
 __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
                                               const __bf16* __restrict__ k,
@@ -64,9 +278,8 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
                                               i64 qss, i64 ksb, i64 ksh, i64 kss, i64 vsb,
                                               i64 vsh, i64 vss, float scale_log2) {
   static_assert(D % 32 == 0 && D <= 256, "head dim must be a multiple of 32");
-  constexpr int KSTEPS = D / 16;          // MFMA k-steps of S^T
-  constexpr int DBLK = D / 32;            // 32-row blocks of O^T
-  constexpr int CHUNKS = D / 8;           // 16-byte chunks per row
+  constexpr int KSTEPS = D / 16;
+  constexpr int DBLK = D / 32;
   __shared__ AttnLds<D> sm;
 
   const int nqb = (sq + kAttnBM - 1) / kAttnBM;
@@ -75,11 +288,10 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
   const int qb = nqb - 1 - id / bh_count;   // heaviest query block first
   const int bh = id % bh_count;
   const int b = bh / heads, h = bh % heads;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
   const int q0 = qb * kAttnBM, qw = q0 + wave * 32;
   const int my_q = qw + l32;
-
   const __bf16* qp = q + b * qsb + h * qsh;
   const __bf16* kp = k + b * ksb + h * ksh;
   const __bf16* vp = v + b * vsb + h * vsh;
@@ -91,185 +303,13 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
     if (my_q < sq) qreg[s] = *(const bf16x8*)(qp + (i64)my_q * qss + 16 * s + 8 * hi);
     else qreg[s] = bf16x8{};
   }
-
   f32x16 oacc[DBLK];
-#pragma unroll
-  for (int a = 0; a < DBLK; ++a) oacc[a] = f32x16{};
-  float m_run = -kInf, l_run = 0.0f;
-
-  int kv_end = sk;
-  if constexpr (CAUSAL) kv_end = min(sk, q0 + kAttnBM);
-  const int ntiles = (kv_end + kAttnBN - 1) / kAttnBN;
-
-  // cooperative tile loads: K as [key][dim] rows, V as 4-key x 8-dim blocks for transposition
-  constexpr int NT = 64 * kAttnWaves;
-  constexpr int KITEMS = kAttnBN * CHUNKS;                  // 16-byte K pieces per tile
-  constexpr int VITEMS = (kAttnBN / 4) * CHUNKS;            // (key quad, dim chunk) V pieces
-  constexpr int KLOADS = (KITEMS + NT - 1) / NT;
-  constexpr int VLOADS = (VITEMS + NT - 1) / NT;
-  u32x4 kbuf[KLOADS];
-  u32x4 vbuf[VLOADS][4];
-
-  auto fetch = [&](int tile) {
-    const int k0 = tile * kAttnBN;
-#pragma unroll
-    for (int i = 0; i < KLOADS; ++i) {
-      const int c = tid + i * NT;
-      const int key = k0 + c / CHUNKS, ch = c % CHUNKS;
-      kbuf[i] = (c < KITEMS && key < sk) ? load16_cached(kp + (i64)key * kss + ch * 8)
-                                         : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int i = 0; i < VLOADS; ++i) {
-      const int c = tid + i * NT;
-      const int ch = c % CHUNKS, quad = c / CHUNKS;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + quad * 4 + r;
-        vbuf[i][r] = (c < VITEMS && key < sk) ? load16_cached(vp + (i64)key * vss + ch * 8)
-                                              : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-  // fp16 staging of V is exact unless a value exceeds fp16's range (65504 after rounding)
-  auto v_overflows = [&]() -> int {
-    int bad = 0;
-#pragma unroll
-    for (int i = 0; i < VLOADS; ++i) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const u32 x = vbuf[i][r][w];
-          // bf16 magnitude bits >= 0x477f (65280 + half ulp region) can round past 65504
-          bad |= ((x & 0x7fffu) >= 0x4780u) | (((x >> 16) & 0x7fffu) >= 0x4780u);
-        }
-      }
-    }
-    return bad;
-  };
-  auto to_f16 = [](u32 bf) -> u32 {  // one bf16 (low 16 bits) -> fp16 bits
-    return half2_bits(__builtin_convertvector(f32x2{as_f32(bf << 16), 0.0f}, half2_t)) & 0xffffu;
-  };
-  auto stash = [&](bool f16v) {
-#pragma unroll
-    for (int i = 0; i < KLOADS; ++i) {
-      const int c = tid + i * NT;
-      const int key = c / CHUNKS, ch = c % CHUNKS;
-      if (c < KITEMS) *(u32x4*)(sm.k + key * AttnLds<D>::KSTRIDE + ch * 8) = kbuf[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VLOADS; ++i) {
-      const int c = tid + i * NT;
-      if (c >= VITEMS) continue;
-      const int ch = c % CHUNKS, quad = c / CHUNKS;
-      // element j of the chunk is head dim ch*8 + j; write the 4 keys of the quad for it
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int word = j >> 1, shift = (j & 1) * 16;
-        u32 e[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          e[r] = (vbuf[i][r][word] >> shift) & 0xffffu;
-          if (f16v) e[r] = to_f16(e[r]);
-        }
-        u32x2 w;
-        w.x = e[0] | (e[1] << 16);
-        w.y = e[2] | (e[3] << 16);
-        *(u32x2*)(sm.vt + (ch * 8 + j) * AttnLds<D>::VSTRIDE + quad * 4) = w;
-      }
-    }
-  };
-
-  if (ntiles > 0) fetch(0);
-  for (int tile = 0; tile < ntiles; ++tile) {
-    // barrier: every wave is done with the previous tile in LDS; also decides the V format
-    const bool f16v = __syncthreads_or(v_overflows()) == 0;
-    stash(f16v);
+  float m_ref, l_run;
+  if (!AttnBlock<D, CAUSAL, true>::run(sm, qreg, kp, vp, kss, vss, sk, q0, qw, my_q,
+                                        scale_log2, oacc, m_ref, l_run)) {
     __syncthreads();
-    if (tile + 1 < ntiles) fetch(tile + 1);
-    const int k0 = tile * kAttnBN;
-    const bool active = !CAUSAL || k0 <= qw + 31;
-    if (!active) continue;
-    // ---- S^T = K Q^T for the two 32-key blocks of the tile
-    f32x16 sacc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sacc[kb] = f32x16{};
-      const __bf16* krow = sm.k + (kb * 32 + l32) * AttnLds<D>::KSTRIDE + 8 * hi;
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        const bf16x8 a = *(const bf16x8*)(krow + 16 * s);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[kb], 0, 0, 0);
-      }
-    }
-    // ---- scale, mask and the running max of this lane's query
-    const bool diag = CAUSAL && (k0 + kAttnBN - 1 > qw);
-    float tmax = -kInf;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-        float t = sacc[kb][r] * scale_log2;
-        if ((diag && key > my_q) || key >= sk) t = -kInf;
-        sacc[kb][r] = t;
-        tmax = __builtin_fmaxf(tmax, t);
-      }
-    }
-    tmax = __builtin_fmaxf(tmax, partner<32>(tmax));
-    const float m_new = __builtin_fmaxf(m_run, tmax);
-    // a fully masked query row (only past the end of the sequence) keeps m = -inf
-    const float alpha = (m_new == -kInf) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-    const float m_use = (m_new == -kInf) ? 0.0f : m_new;
-    float psum = 0.0f;
-    u32 pk[2][8];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(sacc[kb][r] - m_use);
-        const float p1 = __builtin_amdgcn_exp2f(sacc[kb][r + 1] - m_use);
-        psum += p0 + p1;
-        pk[kb][r >> 1] = f16v ? pack_f16x2(p0, p1) : pack_bf16x2(p0, p1);
-      }
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int a = 0; a < DBLK; ++a) oacc[a] *= alpha;
-    // ---- O^T += V^T P^T over the 4 key steps (16 keys each) of the tile
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int kb = c >> 1, half = c & 1;
-      u32x4 bw;
-      bw.x = pk[kb][4 * half + 0];
-      bw.y = pk[kb][4 * half + 1];
-      bw.z = pk[kb][4 * half + 2];
-      bw.w = pk[kb][4 * half + 3];
-      const int kbase = kb * 32 + 16 * half + 4 * hi;
-      if (f16v) {
-        const f16x8 bop = __builtin_bit_cast(f16x8, bw);
-#pragma unroll
-        for (int a = 0; a < DBLK; ++a) {
-          const _Float16* vrow = (const _Float16*)sm.vt + (a * 32 + l32) * AttnLds<D>::VSTRIDE + kbase;
-          const f16x4 lo = *(const f16x4*)(vrow);
-          const f16x4 up = *(const f16x4*)(vrow + 8);
-          const f16x8 aop = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
-          oacc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop, bop, oacc[a], 0, 0, 0);
-        }
-      } else {
-        const bf16x8 bop = __builtin_bit_cast(bf16x8, bw);
-#pragma unroll
-        for (int a = 0; a < DBLK; ++a) {
-          const __bf16* vrow = sm.vt + (a * 32 + l32) * AttnLds<D>::VSTRIDE + kbase;
-          const bf16x4 lo = *(const bf16x4*)(vrow);
-          const bf16x4 up = *(const bf16x4*)(vrow + 8);
-          const bf16x8 aop = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
-          oacc[a] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop, bop, oacc[a], 0, 0, 0);
-        }
-      }
-    }
+    AttnBlock<D, CAUSAL, false>::run(sm, qreg, kp, vp, kss, vss, sk, q0, qw, my_q,
+                                     scale_log2, oacc, m_ref, l_run);
   }
   // ---- readout: O / l, and the natural-log LSE of the scaled scores
   const float l_tot = l_run + partner<32>(l_run);
@@ -287,7 +327,7 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
       }
     }
     if (lse != nullptr && hi == 0)
-      lse[(i64)bh * sq + my_q] = (m_run + __builtin_log2f(l_tot)) * 0.6931471805599453f;
+      lse[(i64)bh * sq + my_q] = (m_ref + __builtin_log2f(l_tot)) * 0.6931471805599453f;
   }
 }
 

@@ -454,9 +454,15 @@ def segment_kernel_name(name: str, var: SegmentVariant) -> str:
 
 
 # ---------------------------------------------------------------- attention fold
-def emit_attention_source(head_dim: int, causal: bool) -> str:
+# Two waves per SIMD for the attention fold: the register budget (<= 256 per lane) that lets
+# one wave's softmax overlap another wave's MFMAs.
+ATTN_WAVES_PER_EU = 2
+
+
+def emit_attention_source(head_dim: int, causal: bool, waves_per_eu: int | None = None) -> str:
     """hiprtc unit of the online-softmax attention fold (no reference counterpart): the
     logsumexp repair exp(s - s2) applied per key tile to (m, l, O)."""
+    wpe = ATTN_WAVES_PER_EU if waves_per_eu is None else waves_per_eu
     if head_dim not in (64, 128):
         raise NotImplementedError("attention fold supports head_dim 64 and 128")
     name = attention_kernel_name(head_dim, causal)
@@ -465,7 +471,7 @@ def emit_attention_source(head_dim: int, causal: bool) -> str:
         f"// online-softmax attention fold: head_dim={head_dim}, causal={causal}; bf16 MFMA, fp32 "
         "running max/sum.\n",
         kernel_header("nep_device.h", "nep_attention.h"),
-        f'extern "C" __global__ void __launch_bounds__(256) {name}(const void* q, const void* k, '
+        f'extern "C" __global__ void __launch_bounds__(256, {wpe}) {name}(const void* q, const void* k, '
         "const void* v, void* o, float* lse, int heads, int sq, int sk, long long qsb, long long qsh, "
         "long long qss, long long ksb, long long ksh, long long kss, long long vsb, long long vsh, "
         "long long vss, float scale_log2) {\n"
