@@ -1,0 +1,46 @@
+"""The C-ABI library: loads, exports every function include/neptune_hip.h declares, compiles
+for gfx950 through hiprtc without a GPU, and reports errors through nep_last_error.
+No compute call is made here (no GPU on the CPU runner)."""
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from neptune_codegen import hip
+
+HEADER = pathlib.Path(__file__).resolve().parent.parent / "include" / "neptune_hip.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(nep_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = hip.load_library()
+    names = declared()
+    assert set(names) == set(hip.EXPORTED), names
+    for name in names:
+        assert getattr(lib, name) is not None
+    assert lib.nep_abi_version() == 1
+
+
+def test_compile_code_object_and_error_reporting():
+    lib = hip.load_library()
+    ok = 'extern "C" __global__ void k(float* x) { x[threadIdx.x] *= 2.0f; }'
+    assert hip.compile_code_object(ok, "ok.hip", ("--offload-arch=gfx950", "-O3"), write_cache=False) > 0
+    with pytest.raises(hip.HipError, match="hiprtc compile"):
+        hip.compile_code_object("this is not C++", "bad.hip", ("--offload-arch=gfx950",), write_cache=False)
+    assert b"bad.hip" in lib.nep_last_error()
+
+
+def test_argument_checks_need_no_gpu():
+    lib = hip.load_library()
+    grid = (ctypes.c_uint32 * 3)(1, 1, 1)
+    block = (ctypes.c_uint32 * 3)(64, 1, 1)
+    assert lib.nep_launch(0, grid, block, 0, None, None, 0) == 1          # NEP_ERR_INVALID
+    assert b"null kernel" in lib.nep_last_error()
+    out = ctypes.c_uint64()
+    assert lib.nep_get_kernel(0, b"k", ctypes.byref(out)) == 1
+    assert lib.nep_compile(None, b"x", b"", None, ctypes.byref(out)) == 1

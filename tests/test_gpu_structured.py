@@ -124,3 +124,74 @@ def test_segment_cfg4_vector_path_bit_exact(dtype):
         got = CG.run_segment_pool(data.to(dev), offsets.to(dev), reduce=reduce, offsets=True).cpu()
         want = R.segment_reference(data, offsets, reduce, offsets=True)
         _bits_equal(got, want)
+
+
+def _raw(t):
+    import numpy as np
+
+    if t.dtype == torch.float32:
+        return t.contiguous().numpy()
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _from_raw(a, dtype):
+    import numpy as np
+
+    if dtype == torch.float32:
+        return torch.from_numpy(a)
+    return torch.from_numpy(a.view(np.int16)).view(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_segment_against_c_oracle_and_device_segment_reduce(dtype):
+    """Bit-exact against the C restatement of the ordered rounding and against torch's own
+    segment_reduce on the device (the CPU-vs-device agreement the reference assumes)."""
+    from oracle import exact as OX
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(9)
+    lengths = torch.poisson(torch.full((512,), 20.0), generator=g).clamp(0, 200).to(torch.int64)
+    lengths[::37] = 0
+    data = (2 * torch.randn(int(lengths.sum()), 128, generator=g)).to(dtype)
+    data[5, 3] = float("inf")
+    data[17, 9] = float("nan")
+    spans = torch.cat([torch.zeros(1, dtype=torch.int64), lengths.cumsum(0)])
+    for reduce, initial in (("sum", None), ("mean", None), ("sum", -2.125), ("mean", 7.0)):
+        _say(f"segment vs C oracle {dtype} {reduce} initial={initial}")
+        got = CG.run_segment_pool(data.to(dev), spans.to(dev), reduce=reduce, offsets=True,
+                                  initial=initial).cpu()
+        want = _from_raw(OX.segment_pool(_raw(data), spans.numpy(), str(dtype).split(".")[1],
+                                         mean=reduce == "mean", initial=initial), dtype)
+        _bits_equal(got, want)
+        on_dev = torch.segment_reduce(data.to(dev), reduce, axis=0, offsets=spans.to(dev),
+                                      initial=initial).cpu()
+        _bits_equal(got, on_dev)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rms_l2_against_c_oracle(dtype):
+    """Against the C restatement of the staged arithmetic (fp32 sum of squares, correctly
+    rounded division and rsqrt, rounding before gamma): equal up to the summation order, so
+    almost every element matches bit for bit; RMS rounds twice (normalized, then times gamma),
+    so a one-ulp difference in the statistics can reach two ulps of the output."""
+    import numpy as np
+
+    from oracle import exact as OX
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(256, 4096, generator=g).to(dtype)
+    gamma = (1 + 0.1 * torch.randn(4096, generator=g)).to(dtype)
+    name = str(dtype).split(".")[1]
+    for which in ("rms", "l2"):
+        _say(f"{which} vs C oracle {dtype}")
+        if which == "rms":
+            got = CG.run_rms_norm(x.to(dev), gamma.to(dev), eps=1e-6).cpu()
+            want = _from_raw(OX.rms_norm(_raw(x), _raw(gamma), name, 1e-6), dtype)
+        else:
+            got = CG.run_l2_normalize(x.to(dev), eps=1e-6).cpu()
+            want = _from_raw(OX.l2_normalize(_raw(x), name, 1e-6), dtype)
+        same = (got.view(torch.int16) == want.view(torch.int16)).float().mean().item()
+        assert same > 0.98, same
+        ulps = (got.view(torch.int16).int() - want.view(torch.int16).int()).abs().max().item()
+        assert ulps <= 2, ulps
