@@ -219,6 +219,19 @@ def cpu_baseline(xs_cpu, seconds_target: float = 15.0):
                       "oracle.references.reference('logsumexp') = torch.logsumexp(x.float(), -1)"}
 
 
+def pmc_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's reading of a plain copy of
+    known size), or None when the summary is absent."""
+    path = ROOT / "profiles" / "logsumexp_bf16_16384x32000_pmc.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -226,6 +239,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-folds", action="store_true", help="skip the per-configuration table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only run the dominant kernel and a 256 MiB copy (3x each), for "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs and their calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; every fold is row/segment-parallel and "
@@ -238,6 +254,16 @@ def main():
 
     dev = torch.device("cuda:0")
     log(f"[bench] device {torch.cuda.get_device_name(dev)}, torch {torch.__version__}")
+    if args.pmc_probe:
+        x = (4 * torch.randn(16384, 32000, generator=seeded(1))).bfloat16().to(dev)
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)   # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            CG.run("logsumexp", x)
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] pmc probe done")
+        return
     xs_cpu, xs = cfg2_inputs(dev)
     widths = (128, 1000, 4096, 32000)
 
@@ -275,7 +301,7 @@ def main():
     dom_bytes = cfg2_bytes(32000)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK, 4), "traffic": pmc_traffic(),
                 "kernel": "logsumexp_serial_bf16 (16384 x 32000)", "kernel_us": round(dom_ms * 1e3, 2),
                 "bytes_per_launch": dom_bytes}
     log(f"[bench] dominant kernel {dom_ms * 1e3:.1f} us, {achieved:.1f} GB/s")
