@@ -5,48 +5,51 @@
 // a new max by exp(m - m') (the logsumexp skeleton's slope exp(s - s2)), so no score matrix is
 // materialised.  Scores live in the base-2 domain t = scale*log2(e) * q.k.
 //
-// Mapping (one workgroup = 4 wave64s = BLOCK_M = 128 queries, 32 per wave; key tiles of 64):
-//  * S^T = K Q^T with v_mfma_f32_32x32x16_bf16: A = K rows (key = lane%32, 8 consecutive head
-//    dims per lane from LDS), B = Q^T (query = lane%32, 8 head dims, held in registers).  The
-//    32x32 result gives lane l the scores of query l%32 for keys 8*(r/4) + 4*(l/32) + r%4, so
-//    the softmax of a query needs its own 32 registers plus one exchange with lane l^32.
-//  * O^T += V^T P^T: B = P^T straight from the score registers, A = V^T read from an LDS copy
-//    of the tile stored transposed ([dim][key]).  The MFMA contraction order over keys is
-//    permuted identically in A and B, which is what lets P^T stay in its accumulator layout.
-//  * P V runs in fp16 (unit roundoff 2^-11, 8x finer than bf16 for P): V is converted
-//    bf16 -> fp16 while staged, exact for |v| < 65536.  If any staged V tile of a query block
-//    holds a larger magnitude, the block is recomputed with P V in bf16 (a second instance of
-//    the loop, so the two modes do not add up in registers).
+// Two kernels per call:
+//  * attention_vt_pack: V [key][dim] bf16 -> per key tile a V^T image in fp16 (the exact MFMA
+//    operand order, XOR-swizzled for conflict-free LDS reads) plus one power-of-two exponent
+//    per tile.  Tiles whose largest |v| reaches 2^15 are stored as v * 2^-e (exact: bf16
+//    values keep their 8 significant bits in fp16 down to |v| >= 2^(e-17)); the fold feeds
+//    such a tile P * 2^e instead of P and weights its row sum by 2^-e, both exact, so no
+//    accumulator is rescaled.  e is capped at 24: |v| >= 2^39 overflows fp16 and yields
+//    inf/NaN rows.  The image is written once per call and read by every query block of the
+//    head.
+//  * attention_fwd: one workgroup = 4 wave64s = BLOCK_M = 128 queries (32 per wave).
+//    K (bf16, the caller's strided rows, bounds-checked buffer loads) and the V^T image go
+//    straight from HBM into double-buffered LDS (buffer_load ... lds, no registers): tile t+1
+//    is in flight while tile t is computed, with one barrier per tile.
+//
+// MFMA mapping (v_mfma_f32_32x32x16_{bf16,f16}):
+//  * S^T = K Q^T: A = K rows (key = lane%32, 8 consecutive head dims per lane from LDS),
+//    B = Q^T (query = lane%32, 8 head dims, registers).  Lane l holds the scores of query l%32
+//    for keys 8*(r/4) + 4*(l/32) + r%4 (register r), so a query's softmax needs its own 32
+//    registers plus one exchange with lane l^32.
+//  * O^T += V^T P^T: B = P^T straight from the score registers (fp16), A = 8 fp16 of V^T row
+//    `dim` for the same keys, which the V^T image stores contiguously.  The contraction order
+//    over keys is permuted identically in A and B.
+//  * P V in fp16 (unit roundoff 2^-11, 8x finer than bf16 for P).
 //  * Lazy rescaling: the reference max only moves when the running max exceeds it by more than
 //    8 (base 2), so P <= 256 (exact range of fp16) and O is rescaled on few tiles.
 //  * The row sum l accumulates the fp16-rounded P with v_dot2 (the values the MFMA multiplies).
 //  * Tiles above the causal diagonal are skipped per wave; workgroups run heaviest query block
-//    first and a head's blocks share one XCD (workgroup id % 8 == head % 8), so its K/V stay in
-//    that XCD's L2.
+//    first and a head's blocks share one XCD (workgroup id % 8 == head % 8), so its K and V^T
+//    stay in that XCD's L2.
 #pragma once
 
 namespace nep {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kAttnBM = 128;           // queries per workgroup
 constexpr int kAttnBN = 64;            // keys per tile
-constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = 256;      // 4 wave64s
 constexpr float kRescaleSlack = 8.0f;  // base-2 headroom before the reference max moves
-
-template <int D>
-struct AttnLds {
-  static constexpr int KSTRIDE = D + 8;         // bf16 per K row (16-byte pad)
-  static constexpr int VSTRIDE = kAttnBN + 4;   // 16-bit words per V^T row (8-byte pad)
-  __bf16 k[kAttnBN * KSTRIDE];
-  u16 vt[D * VSTRIDE];
-};
+constexpr u32 kRawBufferWord3 = 0x00020000u;   // gfx9 raw buffer descriptor, dword 3
+constexpr u32 kVtScaleFrom = 142u;     // bf16 biased exponent of 2^15: tiles at or above scale
 
 __device__ __forceinline__ u32 pack_bf16x2(float a, float b) {
   f32x2 f = {a, b};
@@ -58,229 +61,129 @@ __device__ __forceinline__ u32 pack_f16x2(float a, float b) {
   half2_t h = __builtin_convertvector(f, half2_t);
   return half2_bits(h);
 }
+// 2^k for |k| <= 126 (exact, built from the exponent field)
+__device__ __forceinline__ float exp2_int(int k) { return as_f32((u32)(127 + k) << 23); }
 
-// Per-query-block state and the key-tile loop, in one P V precision.
-template <int D, bool CAUSAL, bool F16V>
-struct AttnBlock {
-  static constexpr int KSTEPS = D / 16;          // MFMA k-steps of S^T
-  static constexpr int DBLK = D / 32;            // 32-row blocks of O^T
-  static constexpr int CHUNKS = D / 8;           // 16-byte chunks per row
-  static constexpr int NT = 64 * kAttnWaves;
-  static constexpr int KITEMS = kAttnBN * CHUNKS;           // 16-byte K pieces per tile
-  static constexpr int VITEMS = (kAttnBN / 4) * CHUNKS;     // (key quad, dim chunk) V pieces
-  static constexpr int KLOADS = (KITEMS + NT - 1) / NT;
-  static constexpr int VLOADS = (VITEMS + NT - 1) / NT;
+// Position (0..63, before the row swizzle) of tile key `key` in a V^T image row: chunk
+// j = 2*(key/16) + (key/4)%2 holds keys 16*(j/2) + 4*(j%2) + {0,1,2,3} and the same + 8, which
+// is the key order of lane (j%2)*32 + .. in the P^T operand of k-step j/2.
+__device__ __forceinline__ int vt_slot(int key) {
+  const int w = key & 15;
+  return ((key >> 4) * 2 + ((w >> 2) & 1)) * 8 + (w & 3) + ((w >> 3) << 2);
+}
 
-  // Runs the block; returns false (after a uniform early exit) if F16V meets an fp16 overflow.
-  __device__ static bool run(AttnLds<D>& sm, const bf16x8* qreg, const __bf16* kp,
-                             const __bf16* vp, i64 kss, i64 vss, int sk, int q0, int qw,
-                             int my_q, float c, f32x16* oacc, float& m_out, float& l_out) {
-    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
-    int kv_end = sk;
-    if constexpr (CAUSAL) kv_end = min(sk, q0 + kAttnBM);
-    const int ntiles = (kv_end + kAttnBN - 1) / kAttnBN;
-#pragma unroll
-    for (int a = 0; a < DBLK; ++a) oacc[a] = f32x16{};
-    float m_ref = -kInf;   // reference max (base 2) of this lane's query
-    float l_run = 0.0f;
+// LDS rows are read 16 bytes per lane, 16 consecutive rows per LDS cycle (64 banks of 4 bytes,
+// 256 bytes per clock).  Row r keeps its 16-byte chunk c at position c ^ swizzle<CH>(r), so the
+// 16 rows of one cycle hit 16 different bank groups: rows of 16+ chunks XOR with r % 16, rows of
+// 8 chunks (128 bytes: two rows per 256-byte bank sweep) XOR with (r / 2) % 8.
+template <int CH>
+__device__ __forceinline__ int swizzle(int row) {
+  static_assert(CH == 8 || CH == 16, "rows of 8 or 16 chunks");
+  if constexpr (CH == 16) return row & 15;
+  else return (row >> 1) & 7;
+}
 
-    u32x4 kbuf[KLOADS];
-    u32x4 vbuf[VLOADS][4];
-    auto fetch = [&](int tile) {
-      const int k0 = tile * kAttnBN;
-#pragma unroll
-      for (int i = 0; i < KLOADS; ++i) {
-        const int cc = tid + i * NT;
-        const int key = k0 + cc / CHUNKS, ch = cc % CHUNKS;
-        kbuf[i] = (cc < KITEMS && key < sk) ? load16_cached(kp + (i64)key * kss + ch * 8)
-                                            : u32x4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int i = 0; i < VLOADS; ++i) {
-        const int cc = tid + i * NT;
-        const int ch = cc % CHUNKS, quad = cc / CHUNKS;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = k0 + quad * 4 + r;
-          vbuf[i][r] = (cc < VITEMS && key < sk) ? load16_cached(vp + (i64)key * vss + ch * 8)
-                                                 : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-    };
-    // any |v| >= 65536 (bf16 magnitude bits >= 0x4780) does not fit fp16
-    auto overflow = [&]() -> int {
-      u32 mx = 0;
-#pragma unroll
-      for (int i = 0; i < VLOADS; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const u32 x = vbuf[i][r][w] & 0x7fff7fffu;
-            mx = max(mx, max(x & 0xffffu, x >> 16));
-          }
-      return mx >= 0x4780u ? 1 : 0;
-    };
-    auto stash = [&]() {
-#pragma unroll
-      for (int i = 0; i < KLOADS; ++i) {
-        const int cc = tid + i * NT;
-        const int key = cc / CHUNKS, ch = cc % CHUNKS;
-        if (cc < KITEMS) *(u32x4*)(sm.k + key * AttnLds<D>::KSTRIDE + ch * 8) = kbuf[i];
-      }
-#pragma unroll
-      for (int i = 0; i < VLOADS; ++i) {
-        const int cc = tid + i * NT;
-        if (cc >= VITEMS) continue;
-        const int ch = cc % CHUNKS, quad = cc / CHUNKS;
-        // head dim ch*8 + j of the 4 keys of the quad -> V^T[dim][quad*4 .. +3]
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int word = j >> 1;
-          u32 e[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) e[r] = vbuf[i][r][word];
-          u32x2 w;
-          if constexpr (F16V) {
-            // bf16 -> fp32 is a shift / mask; two fp32 -> one packed fp16 pair (exact here)
-            if (j & 1) {
-              w.x = pack_f16x2(as_f32(e[0] & 0xffff0000u), as_f32(e[1] & 0xffff0000u));
-              w.y = pack_f16x2(as_f32(e[2] & 0xffff0000u), as_f32(e[3] & 0xffff0000u));
-            } else {
-              w.x = pack_f16x2(as_f32(e[0] << 16), as_f32(e[1] << 16));
-              w.y = pack_f16x2(as_f32(e[2] << 16), as_f32(e[3] << 16));
-            }
-          } else {
-            if (j & 1) {
-              w.x = (e[0] >> 16) | (e[1] & 0xffff0000u);
-              w.y = (e[2] >> 16) | (e[3] & 0xffff0000u);
-            } else {
-              w.x = (e[0] & 0xffffu) | (e[1] << 16);
-              w.y = (e[2] & 0xffffu) | (e[3] << 16);
-            }
-          }
-          *(u32x2*)(sm.vt + (ch * 8 + j) * AttnLds<D>::VSTRIDE + quad * 4) = w;
-        }
-      }
-    };
+// V bf16 [keys, D] of one head -> fp16 V^T tile images [ntiles][D][64] (16-byte chunk j of row
+// d stored at chunk j ^ swizzle<8>(d)) and one exponent per tile.  Keys past sk are zero.
+template <int D>
+__device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
+                                                  u16* __restrict__ vt, int* __restrict__ exps,
+                                                  int heads, int sk, i64 vsb, i64 vsh, i64 vss) {
+  constexpr int CH = D / 8;                         // 16-byte chunks per key row
+  constexpr int UNITS = (kAttnBN / 2) * CH;         // (key pair, dim chunk) units
+  constexpr int UPT = UNITS / kAttnThreads;
+  static_assert(UNITS % kAttnThreads == 0, "head dim must be 64 or 128");
+  __shared__ __attribute__((aligned(16))) u16 img[D * kAttnBN];
+  __shared__ u32 wave_max[kAttnThreads / 64];
+  const int ntiles = (sk + kAttnBN - 1) / kAttnBN;
+  const int bh = blockIdx.x / ntiles, t = blockIdx.x % ntiles;
+  const int b = bh / heads, h = bh % heads;
+  const __bf16* vp = v + b * vsb + h * vsh;
+  const int k0 = t * kAttnBN, tid = threadIdx.x;
 
-    if (ntiles > 0) fetch(0);
-    for (int tile = 0; tile < ntiles; ++tile) {
-      // barrier: every wave is done with the previous tile in LDS (and, in fp16 mode, the
-      // workgroup agrees on whether this V tile fits fp16)
-      if constexpr (F16V) {
-        if (__syncthreads_or(overflow())) return false;
-      } else {
-        __syncthreads();
-      }
-      stash();
-      __syncthreads();
-      if (tile + 1 < ntiles) fetch(tile + 1);
-      const int k0 = tile * kAttnBN;
-      if (CAUSAL && k0 > qw + 31) continue;   // tile entirely above this wave's diagonal
-      // ---- S^T = K Q^T for the two 32-key blocks of the tile
-      f32x16 sacc[2];
+  u32x4 raw[UPT][2];
+  u32 mx = 0;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        sacc[kb] = f32x16{};
-        const __bf16* krow = sm.k + (kb * 32 + l32) * AttnLds<D>::KSTRIDE + 8 * hi;
+  for (int u = 0; u < UPT; ++u) {
+    const int unit = tid + u * kAttnThreads, kp = unit / CH, ch = unit % CH;
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-          const bf16x8 a = *(const bf16x8*)(krow + 16 * s);
-          sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[kb], 0, 0, 0);
-        }
-      }
-      // ---- masks only on the diagonal tile and the ragged last tile
-      const bool need_mask = (CAUSAL && k0 + kAttnBN - 1 > qw) || (k0 + kAttnBN > sk);
-      if (need_mask) {
+    for (int r = 0; r < 2; ++r) {
+      const int key = k0 + 2 * kp + r;
+      raw[u][r] = key < sk ? load16_cached(vp + (i64)key * vss + ch * 8) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-            if ((CAUSAL && key > my_q) || key >= sk) sacc[kb][r] = -kInf;
-          }
-      }
-      float tmax = -kInf;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) tmax = __builtin_fmaxf(tmax, sacc[kb][r]);
-      tmax = __builtin_fmaxf(tmax, partner<32>(tmax)) * c;
-      // move the reference max only when P would exceed 2^8 (or on the first finite tile)
-      const bool move = tmax > m_ref + kRescaleSlack;
-      if (__builtin_amdgcn_ballot_w64(move) != 0) {
-        const float m_new = move ? tmax : m_ref;
-        const float alpha = (m_ref == -kInf) ? 0.0f : __builtin_amdgcn_exp2f(m_ref - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int a = 0; a < DBLK; ++a) oacc[a] *= alpha;
-        m_ref = m_new;
-      }
-      const float shift = (m_ref == -kInf) ? 0.0f : m_ref;
-      u32 pk[2][8];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r], c, -shift));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r + 1], c, -shift));
-          if constexpr (F16V) {
-            const u32 w = pack_f16x2(p0, p1);
-            pk[kb][r >> 1] = w;
-            l_run = __builtin_amdgcn_fdot2(as_half2(w), half2_t{(_Float16)1.0f, (_Float16)1.0f},
-                                           l_run, false);
-          } else {
-            pk[kb][r >> 1] = pack_bf16x2(p0, p1);
-            l_run += p0 + p1;
-          }
-        }
-      // ---- O^T += V^T P^T over the 4 key steps (16 keys each) of the tile
-#pragma unroll
-      for (int cs = 0; cs < 4; ++cs) {
-        const int kb = cs >> 1, half = cs & 1;
-        u32x4 bw;
-        bw.x = pk[kb][4 * half + 0];
-        bw.y = pk[kb][4 * half + 1];
-        bw.z = pk[kb][4 * half + 2];
-        bw.w = pk[kb][4 * half + 3];
-        const int kbase = kb * 32 + 16 * half + 4 * hi;
-#pragma unroll
-        for (int a = 0; a < DBLK; ++a) {
-          const u16* vrow = sm.vt + (a * 32 + l32) * AttnLds<D>::VSTRIDE + kbase;
-          const u32x2 lo = *(const u32x2*)(vrow);
-          const u32x2 up = *(const u32x2*)(vrow + 8);
-          const u32x4 av = {lo.x, lo.y, up.x, up.y};
-          if constexpr (F16V) {
-            oacc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, av),
-                                                             __builtin_bit_cast(f16x8, bw),
-                                                             oacc[a], 0, 0, 0);
-          } else {
-            oacc[a] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av),
-                                                              __builtin_bit_cast(bf16x8, bw),
-                                                              oacc[a], 0, 0, 0);
-          }
-        }
+      for (int w = 0; w < 4; ++w) {
+        const u32 x = raw[u][r][w] & 0x7fff7fffu;
+        mx = max(mx, max(x & 0xffffu, x >> 16));
       }
     }
-    m_out = m_ref;
-    l_out = l_run;
-    return true;
   }
-};
+  // largest bf16 magnitude of the tile (integer order = magnitude order, NaN above inf)
+  mx = max(mx, partner_u32<1>(mx));
+  mx = max(mx, partner_u32<2>(mx));
+  mx = max(mx, partner_u32<4>(mx));
+  mx = max(mx, partner_u32<8>(mx));
+  mx = max(mx, partner_u32<16>(mx));
+  mx = max(mx, partner_u32<32>(mx));
+  if ((tid & 63) == 0) wave_max[tid >> 6] = mx;
+  __syncthreads();
+  mx = max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]));
+  const u32 ebits = mx >> 7;
+  const int e = ebits >= kVtScaleFrom ? min((int)(ebits - kVtScaleFrom + 1), 24) : 0;
+  const float down = exp2_int(-e);
+
+#pragma unroll
+  for (int u = 0; u < UPT; ++u) {
+    const int unit = tid + u * kAttnThreads, kp = unit / CH, ch = unit % CH;
+    const int slot = vt_slot(2 * kp);             // keys 2kp, 2kp+1 are adjacent slots
+#pragma unroll
+    for (int d2 = 0; d2 < 8; ++d2) {
+      const int dim = ch * 8 + d2;
+      const u32 w0 = raw[u][0][d2 >> 1], w1 = raw[u][1][d2 >> 1];
+      const u32 b0 = (d2 & 1) ? (w0 & 0xffff0000u) : (w0 << 16);
+      const u32 b1 = (d2 & 1) ? (w1 & 0xffff0000u) : (w1 << 16);
+      const u32 word = pack_f16x2(as_f32(b0) * down, as_f32(b1) * down);
+      const int pos = (((slot >> 3) ^ swizzle<8>(dim)) << 3) | (slot & 7);
+      *(u32*)(img + dim * kAttnBN + pos) = word;
+    }
+  }
+  __syncthreads();
+  u16* dst = vt + ((i64)bh * ntiles + t) * (D * kAttnBN);
+#pragma unroll
+  for (int c = tid; c < D * kAttnBN / 8; c += kAttnThreads)
+    store16(dst + c * 8, *(const u32x4*)(img + c * 8));
+  if (tid == 0) exps[bh * ntiles + t] = e;
+}
+
+// LDS-DMA of one tile operand: 16 bytes per lane into 1 KB blocks; piece i of wave w fills
+// block i*4 + w.  `dst` is the wave's block (wave-uniform, it becomes M0).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* dst, int voffset,
+                                      int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)dst, 16, voffset, soffset, 0, 0);
+}
 
 template <int D, bool CAUSAL>
 __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
                                               const __bf16* __restrict__ k,
-                                              const __bf16* __restrict__ v,
+                                              const u16* __restrict__ vt,
+                                              const int* __restrict__ exps,
                                               __bf16* __restrict__ o, float* __restrict__ lse,
                                               int heads, int sq, int sk, i64 qsb, i64 qsh,
-                                              i64 qss, i64 ksb, i64 ksh, i64 kss, i64 vsb,
-                                              i64 vsh, i64 vss, float scale_log2) {
-  static_assert(D % 32 == 0 && D <= 256, "head dim must be a multiple of 32");
-  constexpr int KSTEPS = D / 16;
-  constexpr int DBLK = D / 32;
-  __shared__ AttnLds<D> sm;
+                                              i64 qss, i64 ksb, i64 ksh, i64 kss,
+                                              float scale_log2) {
+  static_assert(D == 64 || D == 128, "head dim must be 64 or 128");
+  constexpr int CH = D / 8;                          // 16-byte chunks per K row
+  constexpr int KSTEPS = D / 16;                     // MFMA k-steps of S^T
+  constexpr int DBLK = D / 32;                       // 32-row blocks of O^T
+  constexpr int TILE = kAttnBN * D * 2;              // bytes of one K tile (= one V^T tile)
+  constexpr int PIECES = TILE / 1024 / 4;            // 1 KB DMA blocks per wave and operand
+  constexpr int KROWS = 1024 * 4 / (CH * 16);        // K rows per DMA round of the 4 waves
+  // Separate arrays per buffer: the compiler then proves that LDS reads of one buffer do not
+  // depend on DMA into the other and does not wait for it.
+  __shared__ __attribute__((aligned(1024))) unsigned char kbuf0[TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char kbuf1[TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char vbuf0[TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char vbuf1[TILE];
 
   const int nqb = (sq + kAttnBM - 1) / kAttnBM;
   const int bh_count = gridDim.x / nqb;
@@ -288,13 +191,17 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
   const int qb = nqb - 1 - id / bh_count;   // heaviest query block first
   const int bh = id % bh_count;
   const int b = bh / heads, h = bh % heads;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
+  const int ksw = swizzle<CH>(l32), vsw = swizzle<8>(l32);   // rows kb*32 + l32, a*32 + l32
   const int q0 = qb * kAttnBM, qw = q0 + wave * 32;
   const int my_q = qw + l32;
   const __bf16* qp = q + b * qsb + h * qsh;
   const __bf16* kp = k + b * ksb + h * ksh;
-  const __bf16* vp = v + b * vsb + h * vsh;
+  const int ntiles_all = (sk + kAttnBN - 1) / kAttnBN;
+  const u16* vth = vt + (i64)bh * ntiles_all * (D * kAttnBN);
+  const int* eh = exps + bh * ntiles_all;
 
   // Q^T operand: query my_q, head dims [16s + 8*hi, +8) for k-step s.
   bf16x8 qreg[KSTEPS];
@@ -303,13 +210,139 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
     if (my_q < sq) qreg[s] = *(const bf16x8*)(qp + (i64)my_q * qss + 16 * s + 8 * hi);
     else qreg[s] = bf16x8{};
   }
+
+  int kv_end = sk;
+  if constexpr (CAUSAL) kv_end = min(sk, q0 + kAttnBM);
+  const int ntiles = (kv_end + kAttnBN - 1) / kAttnBN;
+
+  // DMA addressing.  LDS chunk L = (i*4 + wave)*64 + lane of a K tile is key L / CH, position
+  // L % CH, and holds head-dim chunk (L % CH) ^ swizzle<CH>(key) of that key; piece i moves
+  // KROWS keys further (KROWS is a multiple of 16, so the swizzle does not depend on i).
+  int koff0;
+  {
+    const int chunk = wave * 64 + lane, key = chunk / CH, p = chunk % CH;
+    koff0 = (int)((i64)key * kss * 2) + ((p ^ swizzle<CH>(key)) << 4);
+  }
+  const int kstep = (int)((i64)KROWS * kss * 2);
+  // K(tile) and V^T(tile) into LDS; keys at or past sk read as zero (buffer range check),
+  // and are masked to -inf anyway.
+  auto issue = [&](int tile, unsigned char* kdst, unsigned char* vdst) {
+    const int k0 = tile * kAttnBN;
+    const int rows = min(kAttnBN, sk - k0);
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(kp + (i64)k0 * kss), (short)0, (int)(((i64)(rows - 1) * kss + D) * 2),
+        (int)kRawBufferWord3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(vth + (i64)tile * (D * kAttnBN)), (short)0, TILE, (int)kRawBufferWord3);
+#pragma unroll
+    for (int i = 0; i < PIECES; ++i) {
+      dma16(rk, kdst + (i * 4 + wave) * 1024, koff0 + i * kstep, 0);
+      dma16(rv, vdst + (i * 4 + wave) * 1024, lane * 16, (i * 4 + wave) * 1024);
+    }
+  };
+  auto wait_dma = []() { __builtin_amdgcn_s_waitcnt(0x0F70); };   // vmcnt(0)
+
   f32x16 oacc[DBLK];
-  float m_ref, l_run;
-  if (!AttnBlock<D, CAUSAL, true>::run(sm, qreg, kp, vp, kss, vss, sk, q0, qw, my_q,
-                                        scale_log2, oacc, m_ref, l_run)) {
+#pragma unroll
+  for (int a = 0; a < DBLK; ++a) oacc[a] = f32x16{};
+  float m_ref = -kInf;   // reference max (base 2) of this lane's query
+  float l_run = 0.0f;
+
+  auto body = [&](int tile, const unsigned char* kt, const unsigned char* vtt) {
+    const int k0 = tile * kAttnBN;
+    if (CAUSAL && k0 > qw + 31) return;   // tile entirely above this wave's diagonal
+    // ---- S^T = K Q^T for the two 32-key blocks of the tile
+    f32x16 sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sacc[kb] = f32x16{};
+      const unsigned char* krow = kt + (kb * 32 + l32) * (CH * 16);
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        const bf16x8 a = *(const bf16x8*)(krow + (((2 * s + hi) ^ ksw) << 4));
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[kb], 0, 0, 0);
+      }
+    }
+    // ---- masks only on the diagonal tile and the ragged last tile
+    if ((CAUSAL && k0 + kAttnBN - 1 > qw) || (k0 + kAttnBN > sk)) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+          if ((CAUSAL && key > my_q) || key >= sk) sacc[kb][r] = -kInf;
+        }
+    }
+    float tmax = -kInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = __builtin_fmaxf(tmax, sacc[kb][r]);
+    tmax = __builtin_fmaxf(tmax, partner<32>(tmax)) * scale_log2;
+    // A V^T tile stored as v * 2^-e gets P' = P * 2^e (exact) and a row-sum weight of 2^-e;
+    // P' <= 2^15 because the reference max is held max(0, e - 7) above its slack position.
+    const int e = eh[tile];
+    const float lift = (float)max(0, e - 7);
+    // move the reference max only when P' would exceed 2^(8 + min(e, 7)), or on the first
+    // finite tile
+    const bool move = tmax + lift > m_ref + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+      const float m_new = move ? tmax + lift : m_ref;
+      const float alpha = (m_ref == -kInf) ? 0.0f : __builtin_amdgcn_exp2f(m_ref - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int a = 0; a < DBLK; ++a) oacc[a] *= alpha;
+      m_ref = m_new;
+    }
+    const float shift = ((m_ref == -kInf) ? 0.0f : m_ref) - (float)e;
+    const u32 h16 = e < 15 ? (u32)(15 - e) << 10 : 1u << (24 - e);   // fp16 2^-e, e <= 24
+    const half2_t w2 = as_half2(h16 | (h16 << 16));
+    u32 pk[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r], scale_log2, -shift));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r + 1], scale_log2, -shift));
+        const u32 w = pack_f16x2(p0, p1);
+        pk[kb][r >> 1] = w;
+        l_run = __builtin_amdgcn_fdot2(as_half2(w), w2, l_run, false);
+      }
+    // ---- O^T += V^T P^T over the 4 key steps (16 keys each) of the tile
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs) {
+      const int kb = cs >> 1, half = cs & 1;
+      u32x4 bw;
+      bw.x = pk[kb][4 * half + 0];
+      bw.y = pk[kb][4 * half + 1];
+      bw.z = pk[kb][4 * half + 2];
+      bw.w = pk[kb][4 * half + 3];
+      const int chunk = ((2 * cs + hi) ^ vsw) << 4;
+#pragma unroll
+      for (int a = 0; a < DBLK; ++a) {
+        const u32x4 av = *(const u32x4*)(vtt + (a * 32 + l32) * (kAttnBN * 2) + chunk);
+        oacc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, av),
+                                                         __builtin_bit_cast(f16x8, bw),
+                                                         oacc[a], 0, 0, 0);
+      }
+    }
+  };
+
+  // Tile t is computed from buffers t % 2 while the DMA of tile t+1 fills the others (last
+  // read in iteration t-1, before this iteration's barrier).  Unrolled by two so every LDS
+  // address names its array.
+  if (ntiles > 0) issue(0, kbuf0, vbuf0);
+  for (int tile = 0; tile < ntiles;) {
+    wait_dma();
     __syncthreads();
-    AttnBlock<D, CAUSAL, false>::run(sm, qreg, kp, vp, kss, vss, sk, q0, qw, my_q,
-                                     scale_log2, oacc, m_ref, l_run);
+    if (tile + 1 < ntiles) issue(tile + 1, kbuf1, vbuf1);
+    body(tile, kbuf0, vbuf0);
+    if (++tile >= ntiles) break;
+    wait_dma();
+    __syncthreads();
+    if (tile + 1 < ntiles) issue(tile + 1, kbuf0, vbuf0);
+    body(tile, kbuf1, vbuf1);
+    ++tile;
   }
   // ---- readout: O / l, and the natural-log LSE of the scaled scores
   const float l_tot = l_run + partner<32>(l_run);

@@ -17,13 +17,16 @@ import math
 import threading
 
 from neptune_codegen import hip
-from neptune_codegen.emitters import BASE_OPTIONS, attention_kernel_name, emit_attention_source
+from neptune_codegen.emitters import (BASE_OPTIONS, attention_kernel_name, attention_pack_kernel_name,
+                                      emit_attention_source)
 
 _PROGRAMS: dict = {}
 _OPS: dict = {}
 _lock = threading.Lock()
 LOG2E = 1.4426950408889634
 BLOCK_M = 128
+BLOCK_N = 64            # keys per tile (one V^T image per tile)
+K_ROW_STRIDE_MAX = 1 << 24   # K rows are addressed with 32-bit byte offsets within a tile
 
 
 def _program(head_dim: int, causal: bool) -> hip.Program:
@@ -82,17 +85,29 @@ def run_attention(q, k, v, *, scale: float | None = None, causal: bool = True,
     if not math.isfinite(scale) or scale <= 0:
         raise ValueError("attention scale must be finite and positive")
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    if k.stride(2) >= K_ROW_STRIDE_MAX:
+        k = k.contiguous()
     device = q.device.index if q.device.index is not None else torch.cuda.current_device()
-    kernel = _program(D, causal).kernel(
-        attention_kernel_name(D, causal),
-        (hip.PTR,) * 5 + (hip.I32,) * 3 + (hip.I64,) * 9 + (hip.F32,), 256, device)
+    Sk = k.shape[2]
+    ntiles = (Sk + BLOCK_N - 1) // BLOCK_N
+    # V^T tile images (fp16, MFMA operand order) and one power-of-two exponent per tile
+    vt = torch.empty((B * H * ntiles * D * BLOCK_N,), dtype=torch.float16, device=q.device)
+    exps = torch.empty((B * H * ntiles,), dtype=torch.int32, device=q.device)
+    prog = _program(D, causal)
+    pack = prog.kernel(attention_pack_kernel_name(D),
+                       (hip.PTR,) * 3 + (hip.I32,) * 2 + (hip.I64,) * 3, 256, device)
+    fold = prog.kernel(attention_kernel_name(D, causal),
+                       (hip.PTR,) * 6 + (hip.I32,) * 3 + (hip.I64,) * 6 + (hip.F32,), 256, device)
+    stream = hip.current_stream(q.device)
+    pack.launch((B * H * ntiles,),
+                (v.data_ptr(), vt.data_ptr(), exps.data_ptr(), H, Sk, v.stride(0), v.stride(1),
+                 v.stride(2)), stream)
     nqb = (Sq + BLOCK_M - 1) // BLOCK_M
-    kernel.launch((nqb * B * H,),
-                  (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                   lse.data_ptr() if lse is not None else 0, H, Sq, k.shape[2],
-                   q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
-                   v.stride(0), v.stride(1), v.stride(2), scale * LOG2E),
-                  hip.current_stream(q.device))
+    fold.launch((nqb * B * H,),
+                (q.data_ptr(), k.data_ptr(), vt.data_ptr(), exps.data_ptr(), out.data_ptr(),
+                 lse.data_ptr() if lse is not None else 0, H, Sq, Sk,
+                 q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+                 scale * LOG2E), stream)
     return (out, lse) if return_lse else out
 
 

@@ -454,31 +454,41 @@ def segment_kernel_name(name: str, var: SegmentVariant) -> str:
 
 
 # ---------------------------------------------------------------- attention fold
-# Two waves per SIMD for the attention fold: the register budget (<= 256 per lane) that lets
-# one wave's softmax overlap another wave's MFMAs.
+# One wave per SIMD for the attention fold: 64 queries per wave need the full register file
+# (VGPRs + AGPRs, 512 per lane); the wave overlaps its own MFMAs with its softmax.
 ATTN_WAVES_PER_EU = 2
 
 
 def emit_attention_source(head_dim: int, causal: bool, waves_per_eu: int | None = None) -> str:
     """hiprtc unit of the online-softmax attention fold (no reference counterpart): the
-    logsumexp repair exp(s - s2) applied per key tile to (m, l, O)."""
+    logsumexp repair exp(s - s2) applied per key tile to (m, l, O).  Holds two kernels: the
+    V^T tile packer and the fold itself."""
     wpe = ATTN_WAVES_PER_EU if waves_per_eu is None else waves_per_eu
     if head_dim not in (64, 128):
         raise NotImplementedError("attention fold supports head_dim 64 and 128")
     name = attention_kernel_name(head_dim, causal)
+    pack = attention_pack_kernel_name(head_dim)
     return "\n".join([
         "// AUTO-GENERATED by neptune_codegen (HIP emitter) -- do not edit.\n"
-        f"// online-softmax attention fold: head_dim={head_dim}, causal={causal}; bf16 MFMA, fp32 "
-        "running max/sum.\n",
+        f"// online-softmax attention fold: head_dim={head_dim}, causal={causal}; bf16 MFMA for "
+        "Q K^T, fp16 MFMA for P V, fp32 running max/sum.\n",
         kernel_header("nep_device.h", "nep_attention.h"),
+        f'extern "C" __global__ void __launch_bounds__(256) {pack}(const void* v, void* vt, int* exps, '
+        "int heads, int sk, long long vsb, long long vsh, long long vss) {\n"
+        f"  nep::attention_vt_pack<{head_dim}>((const __bf16*)v, (nep::u16*)vt, exps, heads, sk, vsb, "
+        "vsh, vss);\n}\n",
         f'extern "C" __global__ void __launch_bounds__(256, {wpe}) {name}(const void* q, const void* k, '
-        "const void* v, void* o, float* lse, int heads, int sq, int sk, long long qsb, long long qsh, "
-        "long long qss, long long ksb, long long ksh, long long kss, long long vsb, long long vsh, "
-        "long long vss, float scale_log2) {\n"
+        "const void* vt, const int* exps, void* o, float* lse, int heads, int sq, int sk, "
+        "long long qsb, long long qsh, long long qss, long long ksb, long long ksh, long long kss, "
+        "float scale_log2) {\n"
         f"  nep::attention_fwd<{head_dim}, {'true' if causal else 'false'}>((const __bf16*)q, "
-        "(const __bf16*)k, (const __bf16*)v, (__bf16*)o, lse, heads, sq, sk, qsb, qsh, qss, ksb, ksh, "
-        "kss, vsb, vsh, vss, scale_log2);\n}\n"])
+        "(const __bf16*)k, (const nep::u16*)vt, exps, (__bf16*)o, lse, heads, sq, sk, qsb, qsh, qss, "
+        "ksb, ksh, kss, scale_log2);\n}\n"])
 
 
 def attention_kernel_name(head_dim: int, causal: bool) -> str:
     return f"attention_fold_d{head_dim}_{'causal' if causal else 'full'}"
+
+
+def attention_pack_kernel_name(head_dim: int) -> str:
+    return f"attention_vt_pack_d{head_dim}"

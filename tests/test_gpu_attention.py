@@ -74,6 +74,30 @@ def test_attention_parity(shape, causal):
     torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_large_values_use_scaled_tiles(causal):
+    """V tiles whose largest |v| reaches 2^15 are packed as v * 2^-e and the fold rescales the
+    accumulator around them.  Covers: a tile with max exactly 2^15 (e = 1), one with 1e6 and
+    tiny values in other dims, the largest bf16 below 2^16 in the ragged last tile, and a
+    tile just below the threshold (e = 0)."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(12)
+    B, H, S, D = 1, 2, 300, 128
+    q = torch.randn(B, H, S, D, generator=g).bfloat16()
+    k = torch.randn(B, H, S, D, generator=g).bfloat16()
+    v = torch.randn(B, H, S, D, generator=g)
+    v[0, 0, 5, 3] = 32768.0                      # tile 0: max exactly 2^15
+    v[0, 0, 70, 0] = 1.0e6                       # tile 1: large ...
+    v[0, 0, 71, 1:9] = 3.0e-4                    # ... next to small values in other dims
+    v[0, 0, 299, 7] = -65280.0                   # ragged tile 4: largest bf16 below 2^16
+    v[0, 1, 130, 2] = 32512.0                    # tile 2 of head 1: just below 2^15
+    v = v.bfloat16()
+    _say(f"attention large-|v| tiles causal={causal}")
+    got = CG.run_attention(q.to(dev), k.to(dev), v.to(dev), causal=causal)
+    want = R.attention_reference(q, k, v, causal=causal)
+    torch.testing.assert_close(got.cpu().float(), want.float(), rtol=1.6e-2, atol=1e-3)
+
+
 def test_attention_strided_layout_and_scale():
     """[B, S, H, D] storage viewed as [B, H, S, D] (the common projection layout)."""
     dev = _dev()
