@@ -33,14 +33,24 @@ __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp
 
 // ---------------------------------------------------------------- storage dtypes
 // bf16 -> fp32 is exact (the high half of an fp32 pattern).  fp32 -> bf16 rounds to nearest
-// even in integer arithmetic, so the result is independent of the shader's float modes; NaN
-// becomes the canonical quiet NaN 0x7fc0 with its sign, as torch's own conversion does.
+// even.  f32_to_bf16_bits is the integer statement of that rounding (NaN -> the canonical
+// quiet NaN 0x7fc0 with its sign, as torch's own conversion does).  The storage paths use the
+// hardware conversion v_cvt_pk_bf16_f32 (two values per instruction), which a GPU test shows
+// bit-identical to f32_to_bf16_bits for all 2^32 non-NaN fp32 inputs under this build's float
+// modes (ties, denormals, overflow, infinities); a NaN stays a NaN, its payload may differ.
 __device__ __forceinline__ float bf16_bits_to_f32(u32 b16) { return as_f32(b16 << 16); }
 __device__ __forceinline__ u32 f32_to_bf16_bits(float f) {
   u32 b = as_u32(f);
   if ((b & 0x7fffffffu) > 0x7f800000u) return ((b >> 16) & 0x8000u) | 0x7fc0u;
   b += 0x7fffu + ((b >> 16) & 1u);
   return b >> 16;
+}
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// (bf16(a) | bf16(b) << 16), round to nearest even, in one v_cvt_pk_bf16_f32
+__device__ __forceinline__ u32 bf16x2_rne(float a, float b) {
+  const f32x2_t f = {a, b};
+  return __builtin_bit_cast(u32, __builtin_convertvector(f, bf16x2_t));
 }
 
 struct F32 {
@@ -62,10 +72,8 @@ struct BF16 {
   typedef u16 T;
   static constexpr int kVec = 8;
   __device__ static __forceinline__ float load(const T* p) { return bf16_bits_to_f32(*p); }
-  __device__ static __forceinline__ void store(T* p, float v) { *p = (u16)f32_to_bf16_bits(v); }
-  __device__ static __forceinline__ float round(float v) {
-    return bf16_bits_to_f32(f32_to_bf16_bits(v));
-  }
+  __device__ static __forceinline__ void store(T* p, float v) { *p = (u16)bf16x2_rne(v, v); }
+  __device__ static __forceinline__ float round(float v) { return as_f32(bf16x2_rne(v, v) << 16); }
   __device__ static __forceinline__ void unpack(const u32x4& w, float* o) {
     o[0] = as_f32(w.x << 16); o[1] = as_f32(w.x & 0xffff0000u);
     o[2] = as_f32(w.y << 16); o[3] = as_f32(w.y & 0xffff0000u);
@@ -74,10 +82,10 @@ struct BF16 {
   }
   __device__ static __forceinline__ u32x4 pack(const float* v) {
     u32x4 w;
-    w.x = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-    w.y = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-    w.z = f32_to_bf16_bits(v[4]) | (f32_to_bf16_bits(v[5]) << 16);
-    w.w = f32_to_bf16_bits(v[6]) | (f32_to_bf16_bits(v[7]) << 16);
+    w.x = bf16x2_rne(v[0], v[1]);
+    w.y = bf16x2_rne(v[2], v[3]);
+    w.z = bf16x2_rne(v[4], v[5]);
+    w.w = bf16x2_rne(v[6], v[7]);
     return w;
   }
 };

@@ -102,25 +102,44 @@ __device__ __forceinline__ void rms_serial(const typename St::T* __restrict__ x,
   const int t = threadIdx.x % TPR;
   const float count = (float)ncols;
   if constexpr (VECTOR) {
-    u32x4 graw[L2 ? 1 : NV];
+    // gamma is staged once per workgroup in LDS and re-read per row: held in registers it
+    // would stay unpacked across the row loop (64 VGPRs per lane) and halve the occupancy.
+    __shared__ u32x4 gsh[L2 ? 1 : NV * TPR];
     if constexpr (!L2) {
+      if (threadIdx.x < TPR) {
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+          const i64 e = (i64)(u * TPR + t) * VEC;
+          gsh[u * TPR + t] = e < ncols ? load16_cached(gamma + e) : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+      __syncthreads();
+    }
+    // Rows are double-buffered in registers: the next row's loads are issued before this
+    // row is reduced and written, so HBM reads stay in flight across the reduction, the
+    // readout and the stores.
+    const i64 step = (i64)gridDim.x * RPW;
+    u32x4 xn[NV];
+    auto fetch = [&](i64 base) {
+      const i64 row = base + threadIdx.x / TPR;
+      const i64 c1 = row < rows ? ncols : 0;
+      const typename St::T* rp = x + (row < rows ? row : 0) * stride_row;
 #pragma unroll
       for (int u = 0; u < NV; ++u) {
         const i64 e = (i64)(u * TPR + t) * VEC;
-        graw[u] = e < ncols ? load16_cached(gamma + e) : u32x4{0u, 0u, 0u, 0u};
+        xn[u] = e < c1 ? load16(rp + e) : u32x4{0u, 0u, 0u, 0u};
       }
-    }
-    for (i64 base = (i64)blockIdx.x * RPW; base < rows; base += (i64)gridDim.x * RPW) {
+    };
+    if ((i64)blockIdx.x * RPW < rows) fetch((i64)blockIdx.x * RPW);
+    for (i64 base = (i64)blockIdx.x * RPW; base < rows; base += step) {
+      asm volatile("" ::: "memory");   // gamma is re-read from LDS for every row
       const i64 row = base + threadIdx.x / TPR;
       const bool live = row < rows;
       const i64 c1 = live ? ncols : 0;
-      const typename St::T* rp = x + (live ? row : 0) * stride_row;
       u32x4 xr[NV];
 #pragma unroll
-      for (int u = 0; u < NV; ++u) {
-        const i64 e = (i64)(u * TPR + t) * VEC;
-        xr[u] = e < c1 ? load16(rp + e) : u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int u = 0; u < NV; ++u) xr[u] = xn[u];
+      if (base + step < rows) fetch(base + step);
       float total = 0.0f;
 #pragma unroll
       for (int u = 0; u < NV; ++u) {
@@ -129,6 +148,10 @@ __device__ __forceinline__ void rms_serial(const typename St::T* __restrict__ x,
 #pragma unroll
         for (int j = 0; j < VEC; ++j) total += v[j] * v[j];
       }
+      // The packed words are re-unpacked for the readout rather than kept as fp32 across the
+      // reduction (the empty asm makes them opaque), which halves the row's registers.
+#pragma unroll
+      for (int u = 0; u < NV; ++u) asm volatile("" : "+v"(xr[u]));
       total = row_sum<TPR>(total, lds);
       const float scale = rms_scale<L2>(total, count, eps);
       typename St::T* op = out + (live ? row : 0) * ncols;
@@ -138,7 +161,7 @@ __device__ __forceinline__ void rms_serial(const typename St::T* __restrict__ x,
         if (e >= c1) continue;
         float v[VEC], g[VEC], y[VEC];
         St::unpack(xr[u], v);
-        if constexpr (!L2) St::unpack(graw[u], g);
+        if constexpr (!L2) St::unpack(gsh[u * TPR + t], g);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) y[j] = rms_readout<St, L2>(v[j], L2 ? 0.0f : g[j], scale);
         store16(op + e, St::pack(y));

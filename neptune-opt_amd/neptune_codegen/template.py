@@ -348,10 +348,13 @@ def _row_variant(flat, gamma, width: int, *, tile: int | None = None) -> RowVari
 
 
 def _persistent_grid(items_per_wg: int, items: int, device) -> int:
+    """Workgroups for the row-resident kernels: one per row block up to 64 per CU, beyond
+    which workgroups loop.  Measured on MI355X at 32768 x 4096 bf16 (8192 row blocks): 8 per CU
+    (looping) 107 us, 16 per CU 105 us, one per row block 89 us."""
     import torch
 
     cus = torch.cuda.get_device_properties(device).multi_processor_count
-    return max(1, min(_grid_1d(items, items_per_wg), cus * 8))
+    return max(1, min(_grid_1d(items, items_per_wg), cus * 64))
 
 
 def launch_rms_norm(kernel, x, gamma, out, *, plan="serial", wrapper=None):
