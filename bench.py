@@ -42,9 +42,22 @@ def seeded(seed):
     return torch.Generator().manual_seed(seed)
 
 
+def settle(replay, seconds: float) -> None:
+    """Replay a captured graph for `seconds` of wall time, untimed.  The GPU leaves its idle
+    clock state over the first ~0.1 s of a burst; launches in that window run up to 12% slow
+    (measured: 178 us vs 157-160 us for the width-32000 fold), so no timed region starts in it."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        replay()
+        torch.cuda.synchronize()
+
+
 def graph_time(fn, replays: int, inner: int = 1, warmup: int = 2) -> float:
     """Mean ms of one fn() call: fn is captured `inner` times into one HIP graph, replayed
-    `replays` times between events recorded on the replay stream."""
+    `replays` times between events recorded on the replay stream (after 50 ms of untimed
+    replays, see `settle`)."""
     import torch
 
     s = torch.cuda.Stream()
@@ -58,8 +71,7 @@ def graph_time(fn, replays: int, inner: int = 1, warmup: int = 2) -> float:
     with torch.cuda.graph(g):
         for i in range(inner):
             fn(i)
-    g.replay()
-    torch.cuda.synchronize()
+    settle(g.replay, 0.05)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(replays):
@@ -282,6 +294,7 @@ def main():
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         step()
+    settle(g.replay, 0.3)
     for _ in range(args.warmup):
         g.replay()
     torch.cuda.synchronize()
