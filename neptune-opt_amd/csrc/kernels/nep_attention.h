@@ -248,7 +248,7 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
   float m_ref = -kInf;   // reference max (base 2) of this lane's query
   float l_run = 0.0f;
 
-  auto body = [&](int tile, const unsigned char* kt, const unsigned char* vtt) {
+  auto body = [&](int tile, const unsigned char* kt, const unsigned char* vtt, int e) {
     const int k0 = tile * kAttnBN;
     if (CAUSAL && k0 > qw + 31) return;   // tile entirely above this wave's diagonal
     // ---- S^T = K Q^T for the two 32-key blocks of the tile
@@ -281,7 +281,6 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
     tmax = __builtin_fmaxf(tmax, partner<32>(tmax)) * scale_log2;
     // A V^T tile stored as v * 2^-e gets P' = P * 2^e (exact) and a row-sum weight of 2^-e;
     // P' <= 2^15 because the reference max is held max(0, e - 7) above its slack position.
-    const int e = eh[tile];
     const float lift = (float)max(0, e - 7);
     // move the reference max only when P' would exceed 2^(8 + min(e, 7)), or on the first
     // finite tile
@@ -331,17 +330,26 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
   // Tile t is computed from buffers t % 2 while the DMA of tile t+1 fills the others (last
   // read in iteration t-1, before this iteration's barrier).  Unrolled by two so every LDS
   // address names its array.
+  // The exponent of tile t+1 is loaded at the top of iteration t, ahead of that iteration's
+  // DMA: vmcnt retires in order, so a later wait on it would also wait for the DMA.
   if (ntiles > 0) issue(0, kbuf0, vbuf0);
+  int e_cur = ntiles > 0 ? eh[0] : 0;
   for (int tile = 0; tile < ntiles;) {
     wait_dma();
     __syncthreads();
+    int e_next = tile + 1 < ntiles ? eh[tile + 1] : 0;
+    __builtin_amdgcn_sched_barrier(0);
     if (tile + 1 < ntiles) issue(tile + 1, kbuf1, vbuf1);
-    body(tile, kbuf0, vbuf0);
+    body(tile, kbuf0, vbuf0, e_cur);
+    e_cur = e_next;
     if (++tile >= ntiles) break;
     wait_dma();
     __syncthreads();
+    e_next = tile + 1 < ntiles ? eh[tile + 1] : 0;
+    __builtin_amdgcn_sched_barrier(0);
     if (tile + 1 < ntiles) issue(tile + 1, kbuf0, vbuf0);
-    body(tile, kbuf1, vbuf1);
+    body(tile, kbuf1, vbuf1, e_cur);
+    e_cur = e_next;
     ++tile;
   }
   // ---- readout: O / l, and the natural-log LSE of the scaled scores
