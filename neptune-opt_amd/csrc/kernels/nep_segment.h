@@ -14,6 +14,12 @@
 // Mapping: vector path -- LPS lanes per segment, each lane owns one 16-byte channel vector,
 // 64/LPS segments per wavefront, UNR token rows prefetched per step; generic path -- one lane
 // per channel, 64-channel tiles, any strides.
+//
+// Descriptor validation (the reference's device-side span asserts, torch_op.py:378-386) is
+// fused into the fold: with `status` non-null, a lane whose span is malformed, or the last
+// segment's lanes when its end differs from `cover` (>= 0: the coverage check of lengths
+// input), store 0 to status[0] (which the caller set to 1).  Every writer stores the same
+// value, so the unordered stores are benign.
 #pragma once
 
 namespace nep {
@@ -88,6 +94,12 @@ __device__ __forceinline__ bool read_span(const SpanT* spans, i64 stride_span, i
   return s >= 0 && e >= s && e <= nrows;
 }
 
+__device__ __forceinline__ void segment_check(int* status, bool valid, i64 seg, i64 nsegments,
+                                              i64 end, i64 cover) {
+  if (status != nullptr && (!valid || (cover >= 0 && seg == nsegments - 1 && end != cover)))
+    status[0] = 0;
+}
+
 template <class St, bool MEAN, bool INIT_NONE>
 __device__ __forceinline__ float segment_readout(float acc, bool valid, i64 start, i64 end) {
   float r = acc;
@@ -105,7 +117,8 @@ __device__ __forceinline__ void segment_vector(const typename St::T* __restrict_
                                                const SpanT* __restrict__ spans,
                                                typename St::T* __restrict__ out, i64 nrows,
                                                i64 channels, i64 nsegments, i64 stride_row,
-                                               i64 stride_span, float initial) {
+                                               i64 stride_span, float initial, int* status,
+                                               i64 cover) {
   constexpr int VEC = St::kVec;
   constexpr int SPW = WG / LPS;  // segments per workgroup
   const int l = threadIdx.x % LPS;
@@ -113,6 +126,7 @@ __device__ __forceinline__ void segment_vector(const typename St::T* __restrict_
   if (seg >= nsegments) return;
   i64 start, end;
   const bool valid = read_span(spans, stride_span, seg, nrows, &start, &end);
+  segment_check(status, valid, seg, nsegments, end, cover);
   SegAcc<St> acc;
   acc.init(St::round(initial));
   if (valid) {
@@ -141,12 +155,13 @@ __device__ __forceinline__ void segment_generic(const typename St::T* __restrict
                                                 typename St::T* __restrict__ out, i64 nrows,
                                                 i64 channels, i64 nsegments, i64 stride_row,
                                                 i64 stride_channel, i64 stride_span,
-                                                float initial) {
+                                                float initial, int* status, i64 cover) {
   const i64 seg = blockIdx.x;
   const i64 c = (i64)blockIdx.y * 64 + (threadIdx.x & 63);
   if (seg >= nsegments || c >= channels) return;
   i64 start, end;
   const bool valid = read_span(spans, stride_span, seg, nrows, &start, &end);
+  segment_check(status, valid, seg, nsegments, end, cover);
   float acc = St::round(initial);
   if (valid) {
     const typename St::T* col = data + c * stride_channel;

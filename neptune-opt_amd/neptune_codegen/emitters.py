@@ -433,18 +433,20 @@ def emit_segment_source(name: str, *, initial=None, offsets=False, plan="serial"
         if var.vector:
             body = (f"nep::segment_vector<{st}, {span_t}, {mean}, {none}, {var.lps}, {var.unroll}, 256>("
                     f"(const {st}::T*)data, (const {span_t}*)spans, ({st}::T*)out, nrows, channels, "
-                    "nsegments, stride_row, stride_span, __builtin_bit_cast(float, kInitialBits));")
+                    "nsegments, stride_row, stride_span, __builtin_bit_cast(float, kInitialBits), "
+                    "status, cover);")
             wg = 256
         else:
             body = (f"nep::segment_generic<{st}, {span_t}, {mean}, {none}, {var.unroll}>("
                     f"(const {st}::T*)data, (const {span_t}*)spans, ({st}::T*)out, nrows, channels, "
                     "nsegments, stride_row, stride_channel, stride_span, "
-                    "__builtin_bit_cast(float, kInitialBits));")
+                    "__builtin_bit_cast(float, kInitialBits), status, cover);")
             wg = 64
         parts.append(
             f'extern "C" __global__ void __launch_bounds__({wg}) {kname}(const void* data, '
             "const void* spans, void* out, long long nrows, long long channels, long long nsegments, "
-            "long long stride_row, long long stride_channel, long long stride_span) {\n"
+            "long long stride_row, long long stride_channel, long long stride_span, int* status, "
+            "long long cover) {\n"
             f"  {body}\n}}\n")
     return "\n".join(parts)
 

@@ -244,7 +244,7 @@ class SegmentProgram:
 
     def kernel(self, var: SegmentVariant, device: int) -> hip.Kernel:
         return self.program(var).kernel(segment_kernel_name(self.name, var),
-                                        (hip.PTR,) * 3 + (hip.I64,) * 6,
+                                        (hip.PTR,) * 3 + (hip.I64,) * 6 + (hip.PTR, hip.I64),
                                         256 if var.vector else 64, device)
 
 
@@ -324,26 +324,55 @@ def _segment_variant(flat, spans, channels: int) -> SegmentVariant:
     return SegmentVariant(dtype, span_dtype, False, 64, 4)
 
 
+DESCRIPTOR_MESSAGE = ("segment descriptor is invalid: lengths must be nonnegative, within data bounds "
+                      "and (unless unsafe) sum to data axis0 size; boundaries must lie within data "
+                      "bounds and be monotonic")
+
+
+def _device_spans(data, segments, *, offsets):
+    """[start, end) boundaries for the fused-validation launch: offsets as given, lengths as an
+    int64 prefix sum (the same values `_segment_spans` builds); no asserts here."""
+    import torch
+
+    if offsets:
+        return segments
+    spans = torch.empty(segments.shape[0] + 1, dtype=torch.int64, device=segments.device)
+    spans[:1].zero_()
+    torch.cumsum(segments, dim=0, dtype=torch.int64, out=spans[1:])
+    return spans
+
+
 def _launch_segment(name, data, segments, params, plan, *, wrapper=None):
+    """The segment op body.  With at least one segment and channel, the reference's span
+    asserts (range, coverage unless unsafe, monotonic) are evaluated inside the fold kernel,
+    which clears a one-word status; one `_assert_async` on it follows, on the same stream.
+    Otherwise the spans are built and asserted exactly as `_segment_spans` does."""
     import torch
 
     shape = validate_segment_inputs(data, segments, reduce=name.removeprefix("segment_"),
                                     plan=plan, **params)
-    spans = _segment_spans(data, segments, offsets=params["offsets"], unsafe=params["unsafe"])
     channels = 1
     for size in data.shape[1:]:
         channels = channels * size
     out = torch.empty(shape, dtype=data.dtype, device=data.device)
-    if (type(shape[0]) is int and shape[0] == 0) or (type(channels) is int and channels == 0):
+    nseg = shape[0]
+    if type(nseg) is int and nseg > 0 and type(channels) is int and channels > 0:
+        spans = _device_spans(data, segments, offsets=params["offsets"])
+        status = torch.ones(1, dtype=torch.int32, device=data.device)
+        cover = -1 if params["offsets"] or params["unsafe"] else data.shape[0]
+        flat = data.reshape(data.shape[0], channels)
+        launch_segment_kernel(compile_segment_reduction(name, params, plan), flat, spans, out,
+                              status=status, cover=cover)
+        torch._assert_async(status, DESCRIPTOR_MESSAGE)
         return out
-    flat = data.reshape(data.shape[0], channels)
-    launch_segment_kernel(compile_segment_reduction(name, params, plan), flat, spans, out)
+    _segment_spans(data, segments, offsets=params["offsets"], unsafe=params["unsafe"])
     return out
 
 
-def launch_segment_kernel(program, flat, spans, out):
-    """The fold launch alone: flat [nrows, channels] data, validated spans [nsegments + 1],
-    out [nsegments, channels] (contiguous).  Callers own the span checks."""
+def launch_segment_kernel(program, flat, spans, out, *, status=None, cover=-1):
+    """The fold launch alone: flat [nrows, channels] data, spans [nsegments + 1], out
+    [nsegments, channels] (contiguous).  `status` (one int32 set to 1, or None) receives 0 when
+    a span is malformed or, with cover >= 0, the last span does not end at `cover`."""
     import torch
 
     channels = flat.shape[1]
@@ -356,7 +385,8 @@ def launch_segment_kernel(program, flat, spans, out):
     else:
         grid = (nseg, -(-channels // 64))
     kernel.launch(grid, (flat.data_ptr(), spans.data_ptr(), out.data_ptr(), flat.shape[0],
-                         channels, nseg, flat.stride(0), flat.stride(1), spans.stride(0)),
+                         channels, nseg, flat.stride(0), flat.stride(1), spans.stride(0),
+                         status.data_ptr() if status is not None else 0, int(cover)),
                   hip.current_stream(flat.device))
 
 

@@ -195,3 +195,42 @@ def test_rms_l2_against_c_oracle(dtype):
         assert same > 0.98, same
         ulps = (got.view(torch.int16).int() - want.view(torch.int16).int()).abs().max().item()
         assert ulps <= 2, ulps
+
+
+def test_segment_fused_descriptor_check_matches_reference_asserts():
+    """The span checks fused into the segment kernel clear the status word exactly when the
+    reference's asserts (range, coverage unless unsafe, monotonic; torch_op.py:378-386, run here
+    on the CPU by _segment_spans) would fail.  Malformed spans issue no loads, so the launches
+    are safe; the status is read back instead of being asserted on the device."""
+    from neptune_codegen import torch_op as TO
+
+    dev = _dev()
+    data = torch.randn(7, 16).half()
+    program = CG.compile_segment_reduction("segment_sum", {"offsets": False})
+    program_off = CG.compile_segment_reduction("segment_sum", {"offsets": True})
+    cases = [([0, 2, 0, 5], False, False), ([7], False, False), ([3, 4], False, False),
+             ([-1, 8], False, False), ([3, 3], False, False), ([8], False, True), ([4, 4], False, True),
+             ([2, 2], False, True), ([5, -1, 3], False, False), ([0, 3, 7], True, False),
+             ([0, 3, 3, 7], True, True), ([-1, 4], True, True), ([0, 8], True, False),
+             ([4, 3], True, True), ([2, 5], True, False), ([0, 7, 6], True, False)]
+    for indices, is_offsets, unsafe in cases:
+        for idx_dtype in (torch.int32, torch.int64):
+            seg = torch.tensor(indices, dtype=idx_dtype)
+            try:
+                TO._segment_spans(data, seg, offsets=is_offsets, unsafe=unsafe)
+                reference_ok = True
+            except RuntimeError:
+                reference_ok = False
+            _say(f"fused descriptor check {indices} offsets={is_offsets} unsafe={unsafe} {idx_dtype}")
+            seg_dev = seg.to(dev)
+            spans = TO._device_spans(data, seg_dev, offsets=is_offsets)
+            nseg = spans.shape[0] - 1
+            out = torch.empty(nseg, 16, dtype=torch.float16, device=dev)
+            status = torch.ones(1, dtype=torch.int32, device=dev)
+            cover = -1 if is_offsets or unsafe else data.shape[0]
+            TO.launch_segment_kernel(program_off if is_offsets else program, data.to(dev), spans, out,
+                                     status=status, cover=cover)
+            assert bool(status.item()) == reference_ok, (indices, is_offsets, unsafe)
+            if reference_ok:
+                want = R.segment_reference(data, seg, "sum", offsets=is_offsets, unsafe=unsafe)
+                _bits_equal(out.cpu(), want)
