@@ -196,7 +196,8 @@ def per_fold(dev, xs_dev):
     tflops = flops / (ms * 1e-3) / 1e12
     folds["cfg5_attention_causal_bf16_4x32x4096x128"] = {
         "us": round(ms * 1e3, 1), "TFLOP_s": round(tflops, 1), "frac_mfma_bf16": round(tflops / BF16_PEAK, 4),
-        "flops": flops, "query_rows_per_s": round(4 * 32 * 4096 / (ms * 1e-3), 1)}
+        "flops": flops, "query_rows_per_s": round(4 * 32 * 4096 / (ms * 1e-3), 1),
+        "rocprof_pmc": attention_pmc()}
     log(f"[bench] cfg5 attention: {folds['cfg5_attention_causal_bf16_4x32x4096x128']}")
     return folds
 
@@ -244,6 +245,84 @@ def pmc_traffic():
     return None
 
 
+READ_PROBE_SRC = r'''
+template <int UNR>
+__device__ void read_sum(const nep::u32x4* __restrict__ x, float* __restrict__ out, long long n16) {
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  float acc = 0.0f;
+  for (; i + (UNR - 1) * stride < n16; i += UNR * stride) {
+    nep::u32x4 w[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) w[u] = nep::load16(x + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+      acc += nep::as_f32(w[u].x) + nep::as_f32(w[u].y) + nep::as_f32(w[u].z) + nep::as_f32(w[u].w);
+  }
+  for (; i < n16; i += stride) acc += nep::as_f32(nep::load16(x + i).x);
+  acc = nep::group_sum<64>(acc);
+  if ((threadIdx.x & 63) == 0) out[blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64] = acc;
+}
+extern "C" __global__ void __launch_bounds__(256) read_sum1(const void* x, float* out, long long n16) {
+  read_sum<1>((const nep::u32x4*)x, out, n16);
+}
+extern "C" __global__ void __launch_bounds__(256) read_sum4(const void* x, float* out, long long n16) {
+  read_sum<4>((const nep::u32x4*)x, out, n16);
+}
+extern "C" __global__ void __launch_bounds__(256) empty_kernel(const void* x, float* out, long long n16) {}
+'''
+
+
+def read_ceiling(dev):
+    """Best cold-cache time of a plain streaming read (16-byte loads, grid-stride, unroll 1 or
+    4, 256..8192 workgroups of 256 lanes) at each fold input size, and the per-launch floor of
+    an empty kernel in a graph: the practical ceilings the folds are read against."""
+    import torch
+
+    from neptune_codegen import hip
+    from neptune_codegen.emitters import BASE_OPTIONS, kernel_header
+
+    prog = hip.Program(kernel_header("nep_device.h") + READ_PROBE_SRC, "read_probe.hip", BASE_OPTIONS)
+    sig = (hip.PTR, hip.PTR, hip.I64)
+    kernels = {n: prog.kernel(n, sig, 256, dev.index or 0) for n in ("read_sum1", "read_sum4", "empty_kernel")}
+    out = torch.empty(1 << 21, device=dev)
+    stream = lambda: hip.current_stream(dev)  # noqa: E731
+    res = {"empty_launch_us": round(1e3 * graph_time(
+        lambda i: kernels["empty_kernel"].launch((1,), (0, out.data_ptr(), 0), stream()),
+        replays=5, inner=20), 2)}
+    for nbytes in (4227072, 33587200, 134250496, 536879104, 1048608768):
+        n16 = nbytes // 16
+        copies = copies_for(nbytes)
+        xs = [torch.empty(n16 * 4, device=dev).normal_() for _ in range(copies)]
+        best = None
+        for name in ("read_sum1", "read_sum4"):
+            for wgs in (256, 512, 1024, 2048, 4096, 8192):
+                ms = graph_time(lambda i, name=name, wgs=wgs: kernels[name].launch(
+                    (wgs,), (xs[i % copies].data_ptr(), out.data_ptr(), n16), stream()),
+                    replays=5, inner=max(20, copies))
+                if best is None or ms < best[0]:
+                    best = (ms, name, wgs)
+        res[str(nbytes)] = {"us": round(best[0] * 1e3, 2), "GB_s": round(nbytes / best[0] / 1e6, 1),
+                            "kernel": best[1], "workgroups": best[2]}
+        log(f"[bench] read ceiling {nbytes} B: {res[str(nbytes)]}")
+        del xs
+    return res
+
+
+def attention_pmc():
+    """MFMA busy fraction and clock of the attention fold from the committed rocprofv3 PMC
+    summary (SQ_VALU_MFMA_BUSY_CYCLES over active cycles x SIMDs), or None when absent."""
+    path = ROOT / "profiles" / "attention_causal_bf16_4x32x4096x128_pmc.md"
+    if not path.exists():
+        return None
+    out = {}
+    for line in path.read_text().splitlines():
+        for key in ("mfma_busy_frac", "clock_ghz_first_call"):
+            if line.startswith(key + ":"):
+                out[key] = float(line.split(":", 1)[1].strip())
+    return out or None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -254,6 +333,12 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run the dominant kernel and a 256 MiB copy (3x each), for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs and their calibration")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="only time a plain streaming-read kernel at the fold input sizes (the "
+                         "practical ceiling the folds are compared against), then exit")
+    ap.add_argument("--attention-probe", action="store_true",
+                    help="only run the cfg5 attention fold (5 calls), for rocprofv3 --pmc runs "
+                         "(MFMA busy cycles, clock)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; every fold is row/segment-parallel and "
@@ -275,6 +360,17 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log("[bench] pmc probe done")
+        return
+    if args.read_ceiling:
+        print(json.dumps({"read_ceiling": read_ceiling(dev)}), flush=True)
+        return
+    if args.attention_probe:
+        g5 = seeded(5)
+        q, k, v = ((torch.randn(4, 32, 4096, 128, generator=g5).bfloat16()).to(dev) for _ in range(3))
+        for _ in range(5):
+            CG.run_attention(q, k, v, causal=True)
+        torch.cuda.synchronize()
+        log("[bench] attention probe done")
         return
     xs_cpu, xs = cfg2_inputs(dev)
     widths = (128, 1000, 4096, 32000)
