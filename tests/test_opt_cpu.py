@@ -1,0 +1,154 @@
+"""neptune_opt on the CPU: apply's transaction, preview, refusals and the A/B decision rule.
+
+The HIP op handle is replaced by a CPU stand-in op defined in this module (the reference's own
+tests use the same device-free pattern, tests/test_neptune_opt.py:1066-1113).  Everything
+above the kernel -- recognition, rewrite, signature renaming, verification, publication --
+runs for real.
+"""
+import sys
+from unittest.mock import patch
+
+import pytest
+import torch
+
+import neptune_opt
+from neptune_opt import ab
+
+RW = sys.modules["neptune_recognize.rewrite"]
+X = torch.randn(16, 64, generator=torch.Generator().manual_seed(1))
+
+
+@torch.library.custom_op("neptune_cpu_standin::lse", mutates_args=())
+def _lse(x: torch.Tensor) -> torch.Tensor:
+    return torch.logsumexp(x, -1)
+
+
+@_lse.register_fake
+def _(x):
+    return x.new_empty(x.shape[:-1])
+
+
+@torch.library.custom_op("neptune_cpu_standin::wrong", mutates_args=())
+def _wrong(x: torch.Tensor) -> torch.Tensor:
+    return torch.logsumexp(x, -1) + 1.0
+
+
+@_wrong.register_fake
+def _(x):
+    return x.new_empty(x.shape[:-1])
+
+
+def _standin(op):
+    return (patch("neptune_codegen.op_handle", lambda *a, **k: op),
+            patch.object(RW, "_launch_config", return_value=(1024, 4)))
+
+
+class Model(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.w = torch.nn.Parameter(torch.randn(64, 32, generator=torch.Generator().manual_seed(2)))
+
+    def forward(self, x):
+        return torch.logsumexp(x @ self.w, dim=-1) * 2.0 + 1
+
+
+def _exported():
+    model = Model().eval()
+    return model, torch.export.export(model, (X,)).run_decompositions()
+
+
+def test_apply_fuses_verifies_and_publishes():
+    model, ep = _exported()
+    a, b = _standin(torch.ops.neptune_cpu_standin.lse.default)
+    with a, b:
+        eligible, reason = neptune_opt.preview(ep)
+        assert [m.skeleton for m in eligible] == ["logsumexp"], reason
+        report = neptune_opt.apply(ep, verify_with=(model, (X,)))
+    assert report and report.verified and report.graph_changed and report.verification_cases == 1
+    assert [f.skeleton for f in report.fusions] == ["logsumexp"]
+    assert report.fusions[0].proof_kind == "exact-symbolic-real-algebra"
+    assert "verified" in report.summary() and neptune_opt.LAST_REPORT is report
+    targets = [str(n.target) for n in ep.graph.nodes if n.op == "call_function"]
+    assert "neptune_cpu_standin.lse.default" in targets and "aten.mm.default" in targets
+    assert not any("amax" in t or "exp.default" in t for t in targets)
+    torch.testing.assert_close(ep.module()(X), model(X))
+
+
+def test_failed_verification_leaves_the_program_untouched():
+    model, ep = _exported()
+    before = str(ep.graph)
+    a, b = _standin(torch.ops.neptune_cpu_standin.wrong.default)
+    with a, b:
+        report = neptune_opt.apply(ep, verify_with=(model, (X,)))
+    assert not report and report.skipped[0][0] == "verify-failed"
+    assert str(ep.graph) == before
+
+
+def test_unverified_apply_says_so():
+    model, ep = _exported()
+    a, b = _standin(torch.ops.neptune_cpu_standin.lse.default)
+    with a, b:
+        report = neptune_opt.apply(ep)
+    assert report.graph_changed and not report.verified
+    assert "unverified" in report.summary()
+
+
+@pytest.mark.parametrize("kwargs,needle", [
+    ({"capabilities": "rms_norm"}, "capabilities"), ({"capabilities": ("rms_norm", "rms_norm")}, "distinct"),
+    ({"max_regions": 0}, "max_regions"), ({"rtol": float("nan")}, "tolerances"),
+    ({"max_ulps": -1}, "max_ulps"), ({"plan": "tiled"}, "plan"),
+    ({"verification_inputs": [[X]]}, "tuple")])
+def test_argument_refusals_are_reported_not_raised(kwargs, needle):
+    model, ep = _exported()
+    before = str(ep.graph)
+    report = neptune_opt.apply(ep, verify_with=(model, (X,)), **kwargs)
+    assert report.skipped and report.skipped[0][0] == "rewrite-failed"
+    assert needle in report.skipped[0][1]
+    assert str(ep.graph) == before
+
+
+def test_fatal_device_errors_propagate():
+    model, ep = _exported()
+
+    def broken(*a, **k):
+        raise RuntimeError("HIP error: hipErrorIllegalAddress (an illegal memory access was encountered)")
+
+    with patch("neptune_codegen.op_handle", broken), patch.object(RW, "_launch_config", return_value=(1024, 4)):
+        with pytest.raises(ab.FatalCudaError):
+            neptune_opt.apply(ep, verify_with=(model, (X,)))
+
+
+def test_nothing_to_fuse_is_a_report():
+    ep = torch.export.export(torch.nn.Linear(4, 4), (torch.randn(2, 4),))
+    report = neptune_opt.apply(ep)
+    assert not report and report.skipped[0][0] == "no-fusion"
+
+
+def test_op_library_surface():
+    assert neptune_opt.op_parameters("softcap_lse") == ("beta",)
+    assert neptune_opt.op_parameters("logsumexp") == ()
+    for name in ("logsumexp", "stable_l2", "softcap_lse", "variance"):
+        assert callable(getattr(neptune_opt, name)) and name in neptune_opt.__all__
+    with pytest.raises(TypeError, match="beta"):
+        neptune_opt.softcap_lse(X)
+    with pytest.raises(RuntimeError, match="experimental"):
+        neptune_opt.backend(None, ())
+
+
+def test_choose_faster_decision_rule():
+    assert ab.choose_faster(1.0, 0.5)[0] is True
+    assert ab.choose_faster(1.0, 0.99)[0] is False           # inside the 3% margin
+    assert "SLOWER" in ab.choose_faster(1.0, 2.0)[2]
+    assert ab.choose_faster(float("nan"), 1.0)[0] is False
+    with pytest.raises(ValueError):
+        ab.choose_faster(1.0, 1.0, margin=-1)
+
+
+def test_compile_best_validates_before_touching_a_device():
+    for kwargs in ({"plans": ()}, {"plans": ("serial", "tiled")}, {"capabilities": "rms_norm"},
+                   {"reps": 0}, {"margin": float("inf")}):
+        with pytest.raises(ValueError):
+            neptune_opt.compile_best(Model(), (X,), **kwargs)
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError, match="GPU"):
+            neptune_opt.compile_best(Model(), (X,))
