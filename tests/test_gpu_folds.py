@@ -144,3 +144,35 @@ def test_custom_op_registration_runs_hip():
     x = torch.randn(4, 300)
     got = op(x.to(dev))
     torch.testing.assert_close(got.cpu(), torch.logsumexp(x / 3.0, -1), rtol=1e-5, atol=1e-6)
+
+
+def test_split_back_to_back_calls_and_graph_replays():
+    """Split-plan calls of different shapes back to back (several virtual rows per workgroup
+    when nparts is small), and several replays of a captured graph with eager calls in
+    between: each result must match the oracle (no state leaks between launches)."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(21)
+    cases = [((64, 262144), 1024), ((37, 300), 256), ((5, 4097), 1024), ((64, 262144), 1024),
+             ((129, 2), 1)]
+    for (rows, cols), block in cases:
+        x = (4 * torch.randn(rows, cols, generator=g)).bfloat16()
+        _say(f"split back to back: [{rows},{cols}] block={block}")
+        _check("logsumexp", x, CG.run("logsumexp", x.to(dev), plan="split", block=block))
+    x = (4 * torch.randn(48, 20000, generator=g)).bfloat16()
+    xd = x.to(dev)
+    out = torch.empty(48, dtype=torch.bfloat16, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out.copy_(CG.run("logsumexp", xd, plan="split"))
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out.copy_(CG.run("logsumexp", xd, plan="split"))
+    for replay in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        _say(f"split graph replay {replay}")
+        _check("logsumexp", x, out)
+        _check("logsumexp", x, CG.run("logsumexp", xd, plan="split"))   # eager in between
