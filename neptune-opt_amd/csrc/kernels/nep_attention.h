@@ -14,7 +14,8 @@
 //    accumulator is rescaled.  e is capped at 24: |v| >= 2^39 overflows fp16 and yields
 //    inf/NaN rows.  The image is written once per call and read by every query block of the
 //    head.
-//  * attention_fwd: one workgroup = 4 wave64s = BLOCK_M = 128 queries (32 per wave).
+//  * attention_fwd: one workgroup = 8 wave64s = BLOCK_M = 256 queries (32 per wave), one
+//    workgroup per CU (two waves per SIMD): each staged K / V^T tile serves 256 queries.
 //    K (bf16, the caller's strided rows, bounds-checked buffer loads) and the V^T image go
 //    straight from HBM into double-buffered LDS (buffer_load ... lds, no registers): tile t+1
 //    is in flight while tile t is computed, with one barrier per tile.
@@ -44,9 +45,10 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kAttnBM = 128;           // queries per workgroup
+constexpr int kAttnWaves = 8;          // wave64s per fold workgroup (32 queries each)
+constexpr int kAttnBM = 32 * kAttnWaves;   // queries per fold workgroup
 constexpr int kAttnBN = 64;            // keys per tile
-constexpr int kAttnThreads = 256;      // 4 wave64s
+constexpr int kAttnThreads = 256;      // V^T pack workgroup: 4 wave64s
 constexpr float kRescaleSlack = 8.0f;  // base-2 headroom before the reference max moves
 constexpr u32 kRawBufferWord3 = 0x00020000u;   // gfx9 raw buffer descriptor, dword 3
 constexpr u32 kVtScaleFrom = 142u;     // bf16 biased exponent of 2^15: tiles at or above scale
@@ -155,7 +157,7 @@ __device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
 }
 
 // LDS-DMA of one tile operand: 16 bytes per lane into 1 KB blocks; piece i of wave w fills
-// block i*4 + w.  `dst` is the wave's block (wave-uniform, it becomes M0).
+// block i*W + w (W waves per workgroup).  `dst` is the wave's block (wave-uniform, it becomes M0).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* dst, int voffset,
                                       int soffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -176,8 +178,9 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
   constexpr int KSTEPS = D / 16;                     // MFMA k-steps of S^T
   constexpr int DBLK = D / 32;                       // 32-row blocks of O^T
   constexpr int TILE = kAttnBN * D * 2;              // bytes of one K tile (= one V^T tile)
-  constexpr int PIECES = TILE / 1024 / 4;            // 1 KB DMA blocks per wave and operand
-  constexpr int KROWS = 1024 * 4 / (CH * 16);        // K rows per DMA round of the 4 waves
+  constexpr int PIECES = TILE / 1024 / kAttnWaves;   // 1 KB DMA blocks per wave and operand
+  constexpr int KROWS = 1024 * kAttnWaves / (CH * 16);   // K rows per DMA round of all waves
+  static_assert(PIECES >= 1 && KROWS % 16 == 0, "DMA mapping");
   // Separate arrays per buffer: the compiler then proves that LDS reads of one buffer do not
   // depend on DMA into the other and does not wait for it.
   __shared__ __attribute__((aligned(1024))) unsigned char kbuf0[TILE];
@@ -215,7 +218,7 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
   if constexpr (CAUSAL) kv_end = min(sk, q0 + kAttnBM);
   const int ntiles = (kv_end + kAttnBN - 1) / kAttnBN;
 
-  // DMA addressing.  LDS chunk L = (i*4 + wave)*64 + lane of a K tile is key L / CH, position
+  // DMA addressing.  LDS chunk L = (i*W + wave)*64 + lane (W waves) of a K tile is key L / CH, position
   // L % CH, and holds head-dim chunk (L % CH) ^ swizzle<CH>(key) of that key; piece i moves
   // KROWS keys further (KROWS is a multiple of 16, so the swizzle does not depend on i).
   int koff0;
@@ -236,8 +239,8 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
         (void*)(vth + (i64)tile * (D * kAttnBN)), (short)0, TILE, (int)kRawBufferWord3);
 #pragma unroll
     for (int i = 0; i < PIECES; ++i) {
-      dma16(rk, kdst + (i * 4 + wave) * 1024, koff0 + i * kstep, 0);
-      dma16(rv, vdst + (i * 4 + wave) * 1024, lane * 16, (i * 4 + wave) * 1024);
+      dma16(rk, kdst + (i * kAttnWaves + wave) * 1024, koff0 + i * kstep, 0);
+      dma16(rv, vdst + (i * kAttnWaves + wave) * 1024, lane * 16, (i * kAttnWaves + wave) * 1024);
     }
   };
   auto wait_dma = []() { __builtin_amdgcn_s_waitcnt(0x0F70); };   // vmcnt(0)

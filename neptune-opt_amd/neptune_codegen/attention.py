@@ -17,14 +17,14 @@ import math
 import threading
 
 from neptune_codegen import hip
-from neptune_codegen.emitters import (BASE_OPTIONS, attention_kernel_name, attention_pack_kernel_name,
-                                      emit_attention_source)
+from neptune_codegen.emitters import (ATTN_FOLD_THREADS, BASE_OPTIONS, attention_kernel_name,
+                                      attention_pack_kernel_name, emit_attention_source)
 
 _PROGRAMS: dict = {}
 _OPS: dict = {}
 _lock = threading.Lock()
 LOG2E = 1.4426950408889634
-BLOCK_M = 128
+BLOCK_M = 256           # queries per fold workgroup (8 waves of 32)
 BLOCK_N = 64            # keys per tile (one V^T image per tile)
 K_ROW_STRIDE_MAX = 1 << 24   # K rows are addressed with 32-bit byte offsets within a tile
 
@@ -97,7 +97,8 @@ def run_attention(q, k, v, *, scale: float | None = None, causal: bool = True,
     pack = prog.kernel(attention_pack_kernel_name(D),
                        (hip.PTR,) * 3 + (hip.I32,) * 2 + (hip.I64,) * 3, 256, device)
     fold = prog.kernel(attention_kernel_name(D, causal),
-                       (hip.PTR,) * 6 + (hip.I32,) * 3 + (hip.I64,) * 6 + (hip.F32,), 256, device)
+                       (hip.PTR,) * 6 + (hip.I32,) * 3 + (hip.I64,) * 6 + (hip.F32,),
+                       ATTN_FOLD_THREADS, device)
     stream = hip.current_stream(q.device)
     pack.launch((B * H * ntiles,),
                 (v.data_ptr(), vt.data_ptr(), exps.data_ptr(), H, Sk, v.stride(0), v.stride(1),

@@ -456,9 +456,9 @@ def segment_kernel_name(name: str, var: SegmentVariant) -> str:
 
 
 # ---------------------------------------------------------------- attention fold
-# One wave per SIMD for the attention fold: 64 queries per wave need the full register file
-# (VGPRs + AGPRs, 512 per lane); the wave overlaps its own MFMAs with its softmax.
+# Two waves per SIMD for the attention fold (one 8-wave workgroup per CU, <= 256 VGPRs).
 ATTN_WAVES_PER_EU = 2
+ATTN_FOLD_THREADS = 512
 
 
 def emit_attention_source(head_dim: int, causal: bool, waves_per_eu: int | None = None) -> str:
@@ -479,7 +479,7 @@ def emit_attention_source(head_dim: int, causal: bool, waves_per_eu: int | None 
         "int heads, int sk, long long vsb, long long vsh, long long vss) {\n"
         f"  nep::attention_vt_pack<{head_dim}>((const __bf16*)v, (nep::u16*)vt, exps, heads, sk, vsb, "
         "vsh, vss);\n}\n",
-        f'extern "C" __global__ void __launch_bounds__(256, {wpe}) {name}(const void* q, const void* k, '
+        f'extern "C" __global__ void __launch_bounds__({ATTN_FOLD_THREADS}, {wpe}) {name}(const void* q, const void* k, '
         "const void* vt, const int* exps, void* o, float* lse, int heads, int sq, int sk, "
         "long long qsb, long long qsh, long long qss, long long ksb, long long ksh, long long kss, "
         "float scale_log2) {\n"
