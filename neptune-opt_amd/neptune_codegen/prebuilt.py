@@ -18,7 +18,7 @@ def _fold_programs():
     shapes = [(8192, 1024, torch.float32)] + [(16384, w, torch.bfloat16) for w in (128, 1000, 4096, 32000)]
     for rows, ncols, dtype in shapes:
         x2 = torch.empty((rows, ncols), device="meta", dtype=dtype)
-        block, warps = best_config(rows, ncols, dtype, None)
+        block, warps = best_config(rows, ncols, dtype, None, device_name="gfx950")
         var = _fold_variant(x2, ncols, block, warps)
         out.append(compile_skeleton("logsumexp", lse).program(var))
     x2 = torch.empty((64, 262144), device="meta", dtype=torch.bfloat16)
@@ -54,5 +54,11 @@ def _segment_programs():
     return out
 
 
+def _attention_programs():
+    from neptune_codegen.attention import _program
+
+    return [_program(128, True), _program(128, False), _program(64, True)]
+
+
 def programs():
-    return _fold_programs() + _row_programs() + _segment_programs()
+    return _fold_programs() + _row_programs() + _segment_programs() + _attention_programs()

@@ -14,8 +14,8 @@ import math
 import threading
 
 from neptune_codegen import hip
-from neptune_codegen.autotune import (UNROLL, best_config, lanes_per_row, parameter_identity,
-                                      parameter_tag, vec_of)
+from neptune_codegen.autotune import (MAX_UNROLL, UNROLL, best_config, lanes_per_row,
+                                      parameter_identity, parameter_tag, vec_of)
 from neptune_codegen.emitters import (BASE_OPTIONS, NO_CONTRACT, FoldVariant, RowVariant,
                                       check_supported, emit_kernel_source, emit_rms_state_source,
                                       fold_kernel_name, rms_kernel_names)
@@ -147,8 +147,9 @@ def _is_vector(x2, ncols: int, vec: int, extra_align: int = 0) -> bool:
 
 
 def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: int = 0) -> FoldVariant:
-    """Launch shape: 16-byte loads when the layout allows, lanes per row from BLOCK,
-    workgroup = max(64 * num_warps, lanes per row)."""
+    """Launch shape: 16-byte loads when the layout allows, lanes per row from BLOCK (a tile
+    wider than the workgroup's lanes gives each lane up to MAX_UNROLL slots first), workgroup =
+    max(64 * num_warps, lanes per row)."""
     vec = vec_of(x2.dtype)
     vector = _is_vector(x2, ncols, vec, split_block)
     if vector and split_block and split_block < vec:
@@ -156,7 +157,11 @@ def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: in
     tpr = lanes_per_row(block, vec if vector else 1)
     waves = max(1, min(16, int(num_warps)))
     waves = 1 << (waves - 1).bit_length()
-    return FoldVariant(str(x2.dtype).replace("torch.", ""), vector, tpr, UNROLL, waves)
+    unroll = UNROLL
+    while tpr > 64 * waves and unroll < MAX_UNROLL and not split_block:
+        tpr //= 2
+        unroll *= 2
+    return FoldVariant(str(x2.dtype).replace("torch.", ""), vector, tpr, unroll, waves)
 
 
 def _grid_1d(items: int, per_wg: int) -> int:
