@@ -487,14 +487,27 @@ __device__ __forceinline__ void fold_split_merge(const float* __restrict__ pm,
   s.seen = 0;
   s.status = 0;
   if (live) {
-    for (i64 p = lane; p < nparts; p += 64) {
-      const i64 slot = row * nparts + p;
-      State c;
-      c.m = pm[slot];
-      c.acc = pa[slot];
-      c.seen = pv[slot];
-      c.status = ps[slot];
-      s = merge_state<F>(s, c);
+    // four partial states per lane are loaded before any is merged, so one memory latency
+    // covers up to 256 parts
+    constexpr int PRE = 4;
+    for (i64 p0 = lane; p0 < nparts; p0 += 64 * PRE) {
+      State c[PRE];
+      bool ok[PRE];
+#pragma unroll
+      for (int u = 0; u < PRE; ++u) {
+        const i64 p = p0 + 64 * u;
+        ok[u] = p < nparts;
+        if (ok[u]) {
+          const i64 slot = row * nparts + p;
+          c[u].m = pm[slot];
+          c[u].acc = pa[slot];
+          c[u].seen = pv[slot];
+          c[u].status = ps[slot];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < PRE; ++u)
+        if (ok[u]) s = merge_state<F>(s, c[u]);
     }
   }
   s = group_merge<F, 64>(s);
