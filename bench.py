@@ -309,6 +309,68 @@ def read_ceiling(dev):
     return res
 
 
+def compile_best_table(dev):
+    """neptune_opt.compile_best on one model per config family: the exported module (AOTI,
+    Inductor-generated kernels) against the package whose recognised regions call the HIP
+    folds.  Each entry: the chosen package, both median times and the decision reason."""
+    import tempfile
+
+    import torch
+
+    import neptune_opt
+
+    class LSE(torch.nn.Module):
+        def forward(self, x):
+            return torch.logsumexp(x, dim=-1)
+
+    class StableL2(torch.nn.Module):
+        def forward(self, x):
+            m = x.abs().amax(dim=-1, keepdim=True).clamp_min(1e-30)
+            return (m * torch.sqrt(((x / m) ** 2).sum(dim=-1, keepdim=True))).squeeze(-1)
+
+    class RMS(torch.nn.Module):
+        def __init__(self, gamma):
+            super().__init__()
+            self.gamma = torch.nn.Parameter(gamma, requires_grad=False)
+
+        def forward(self, x):
+            z = x.to(torch.float32)
+            return (z * torch.rsqrt(z.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype) * self.gamma
+
+    class SegMean(torch.nn.Module):
+        def forward(self, data, offsets):
+            return torch.segment_reduce(data, "mean", offsets=offsets)
+
+    g = seeded(11)
+    lengths = torch.poisson(torch.full((65536,), 20.0), generator=seeded(4)).clamp(0, 200).to(torch.int64)
+    offsets = torch.cat([torch.zeros(1, dtype=torch.int64), lengths.cumsum(0)])
+    cases = [
+        ("cfg1 logsumexp fp32 8192x1024", LSE(), ((3 * torch.randn(8192, 1024, generator=g)),), ()),
+        ("cfg2 logsumexp bf16 16384x32000", LSE(), ((4 * torch.randn(16384, 32000, generator=g)).bfloat16(),), ()),
+        ("stable_l2 fp32 16384x4096", StableL2(), (torch.randn(16384, 4096, generator=g),), ()),
+        ("cfg3 rms_norm bf16 32768x4096", RMS((1 + 0.1 * torch.randn(4096, generator=g)).bfloat16()),
+         (torch.randn(32768, 4096, generator=g).bfloat16(),), ("rms_norm",)),
+        ("cfg4 segment_mean fp16 65536 segments", SegMean(),
+         (torch.randn(int(lengths.sum()), 128, generator=g).half(), offsets), ("segment_pool",)),
+    ]
+    table = {}
+    for name, module, args, caps in cases:
+        module = module.to(dev).eval()
+        args = tuple(a.to(dev) for a in args)
+        with tempfile.TemporaryDirectory(prefix="neptune_cb_") as directory:
+            log(f"[bench] compile_best: {name}")
+            choice = neptune_opt.compile_best(module, args, package_dir=directory, capabilities=caps,
+                                              reps=10, rounds=5, verbose=False)
+        table[name] = {"used_fusion": choice.used_fusion, "baseline_ms": round(choice.baseline_ms, 4),
+                       "fused_ms": round(choice.fused_ms, 4), "speedup": round(choice.speedup, 3),
+                       "fusions": [str(f) for f in getattr(choice.report, "fusions", [])],
+                       "reason": choice.reason}
+        log(f"[bench] compile_best {name}: {table[name]}")
+        del module, args
+        torch.cuda.empty_cache()
+    return table
+
+
 def attention_pmc():
     """MFMA busy fraction and clock of the attention fold from the committed rocprofv3 PMC
     summary (SQ_VALU_MFMA_BUSY_CYCLES over active cycles x SIMDs), or None when absent."""
@@ -336,6 +398,9 @@ def main():
     ap.add_argument("--read-ceiling", action="store_true",
                     help="only time a plain streaming-read kernel at the fold input sizes (the "
                          "practical ceiling the folds are compared against), then exit")
+    ap.add_argument("--compile-best", action="store_true",
+                    help="only run neptune_opt.compile_best (AOTI baseline vs fused package, "
+                         "verified and A/B timed) on models built around the configs, then exit")
     ap.add_argument("--attention-probe", action="store_true",
                     help="only run the cfg5 attention fold (5 calls), for rocprofv3 --pmc runs "
                          "(MFMA busy cycles, clock)")
@@ -363,6 +428,9 @@ def main():
         return
     if args.read_ceiling:
         print(json.dumps({"read_ceiling": read_ceiling(dev)}), flush=True)
+        return
+    if args.compile_best:
+        print(json.dumps({"compile_best": compile_best_table(dev)}), flush=True)
         return
     if args.attention_probe:
         g5 = seeded(5)

@@ -18,6 +18,9 @@
  *   nep_launch               replaces kernel[grid](args..., BLOCK=, num_warps=)
  *                            (template.py:377-390, template.py:307-319, torch_op.py:406-409):
  *                            asynchronous launch on the caller's stream, no synchronisation.
+ *   nep_launch_packed        the same launch with the arguments already packed into one kernarg
+ *                            image (what Triton's generated launcher builds per call); the host
+ *                            cost per launch is one call, with no per-argument pointer array.
  *   nep_last_error           the text the reference surfaces through Python exceptions; it
  *                            carries the HIP error name so that fatal-error classification by
  *                            message (neptune_opt/ab.py:23-44) keeps working.
@@ -84,6 +87,15 @@ int nep_get_kernel(uint64_t module, const char* kernel_name, uint64_t* kernel_ou
  */
 int nep_launch(uint64_t kernel, const uint32_t grid[3], const uint32_t block[3],
                uint32_t lds_bytes, void* stream, void** args, size_t nargs);
+
+/*
+ * Launch `kernel` on a grid of (gx, gy, gz) workgroups of `block` work-items (1-D), with
+ * `lds_bytes` of dynamic LDS, on `stream`.  `args` is the kernel's explicit-argument image:
+ * every parameter at its natural alignment in declaration order (C struct layout), `nbytes`
+ * long; the runtime appends the hidden arguments itself.
+ */
+int nep_launch_packed(uint64_t kernel, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block,
+                      uint32_t lds_bytes, void* stream, const void* args, size_t nbytes);
 
 /* Name of the current device's ISA (e.g. "gfx950:sramecc+:xnack-") into buf. */
 int nep_device_arch(char* buf, size_t buf_len);

@@ -130,7 +130,7 @@ std::map<std::tuple<int, std::string, std::string>, hipModule_t> g_modules;
 
 extern "C" {
 
-int nep_abi_version(void) { return 1; }
+int nep_abi_version(void) { return 2; }
 
 const char* nep_last_error(void) { return g_last_error.c_str(); }
 
@@ -218,6 +218,25 @@ int nep_launch(uint64_t kernel, const uint32_t grid[3], const uint32_t block[3],
                                          grid[1], grid[2], block[0], block[1], block[2],
                                          lds_bytes, reinterpret_cast<hipStream_t>(stream), args,
                                          nullptr);
+  if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel");
+  return NEP_OK;
+}
+
+int nep_launch_packed(uint64_t kernel, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block,
+                      uint32_t lds_bytes, void* stream, const void* args, size_t nbytes) {
+  if (kernel == 0) return fail(NEP_ERR_INVALID, "nep_launch_packed: null kernel");
+  if (nbytes != 0 && args == nullptr)
+    return fail(NEP_ERR_INVALID, "nep_launch_packed: nbytes > 0 but args is null");
+  if (gx == 0 || gy == 0 || gz == 0) return fail(NEP_ERR_INVALID, "nep_launch_packed: empty grid");
+  if (block == 0 || block > 1024)
+    return fail(NEP_ERR_INVALID, "nep_launch_packed: workgroup size must be in [1, 1024]");
+  size_t size = nbytes;
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(args),
+                    HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+  hipError_t err = hipModuleLaunchKernel(reinterpret_cast<hipFunction_t>(kernel), gx, gy, gz,
+                                         block, 1, 1, lds_bytes,
+                                         reinterpret_cast<hipStream_t>(stream), nullptr,
+                                         nbytes != 0 ? config : nullptr);
   if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel");
   return NEP_OK;
 }

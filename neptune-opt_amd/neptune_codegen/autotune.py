@@ -155,11 +155,39 @@ def default_config(rows, ncols, dtype=None) -> tuple:
     return block, 4
 
 
+_CHOICES: dict = {}
+_CHOICES_MAX = 4096
+
+
+def _table_token():
+    try:
+        from neptune_codegen import launch_table
+    except Exception:  # noqa: BLE001
+        return None
+    return id(getattr(launch_table, "TABLES", None))
+
+
 def best_config(rows, ncols, dtype=None, device=None, device_name=None,
                 verbose: bool = False) -> tuple:
-    """`(BLOCK, num_warps)` for a row length on this machine: measured entry, else default."""
+    """`(BLOCK, num_warps)` for a row length on this machine: measured entry, else default.
+
+    The answer depends on the row class, the width, the dtype, the machine and the launch
+    table, so it is memoised on exactly those (a replaced table is a new key)."""
     if not isinstance(rows, int) or not isinstance(ncols, int):
         return DEFAULT
+    if not verbose:
+        key = (rows_class(rows), ncols, str(dtype), str(device), device_name, _table_token())
+        cfg = _CHOICES.get(key)
+        if cfg is None:
+            cfg = _best_config(rows, ncols, dtype, device, device_name, False)
+            if len(_CHOICES) >= _CHOICES_MAX:
+                _CHOICES.clear()
+            _CHOICES[key] = cfg
+        return cfg
+    return _best_config(rows, ncols, dtype, device, device_name, verbose)
+
+
+def _best_config(rows, ncols, dtype, device, device_name, verbose) -> tuple:
     if device is not None and str(device).split(":", 1)[0] != "cuda":
         return default_config(rows, ncols, dtype)
     if device_name is None:

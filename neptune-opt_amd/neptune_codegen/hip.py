@@ -10,6 +10,7 @@ import ctypes
 import hashlib
 import os
 import pathlib
+import struct
 import threading
 
 PACKAGE_DIR = pathlib.Path(__file__).resolve().parent
@@ -18,7 +19,7 @@ CACHE_DIR = PACKAGE_DIR / "_codeobj"
 
 NEP_OK = 0
 EXPORTED = ("nep_abi_version", "nep_last_error", "nep_compile", "nep_compile_code_object",
-            "nep_free", "nep_get_kernel", "nep_launch", "nep_device_arch")
+            "nep_free", "nep_get_kernel", "nep_launch", "nep_launch_packed", "nep_device_arch")
 
 _lock = threading.Lock()
 _lib = None
@@ -64,9 +65,13 @@ def load_library(require_torch: bool = True) -> ctypes.CDLL:
                                    ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
                                    ctypes.c_size_t]
         lib.nep_launch.restype = ctypes.c_int
+        u32 = ctypes.c_uint32
+        lib.nep_launch_packed.argtypes = [ctypes.c_uint64, u32, u32, u32, u32, u32,
+                                          ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+        lib.nep_launch_packed.restype = ctypes.c_int
         lib.nep_device_arch.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
         lib.nep_device_arch.restype = ctypes.c_int
-        if lib.nep_abi_version() != 1:
+        if lib.nep_abi_version() != 2:
             raise RuntimeError("libneptune_hip ABI version mismatch; rebuild the library")
         _lib = lib
         return lib
@@ -138,23 +143,41 @@ def get_kernel(module: int, kernel_name: str) -> int:
 PTR, I64, I32, F32 = ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_float
 
 
-class Kernel:
-    """A loaded extern "C" kernel with a fixed argument signature."""
+_ARG_CODES = {ctypes.c_void_p: "P", ctypes.c_longlong: "q", ctypes.c_int: "i",
+              ctypes.c_float: "f"}
 
-    __slots__ = ("handle", "name", "argtypes", "block", "lds")
+
+class Kernel:
+    """A loaded extern "C" kernel with a fixed argument signature.
+
+    Arguments are packed into the kernel's explicit-argument image with `struct` in native
+    mode ('@': every field at its natural alignment, C struct layout -- the layout the AMDGPU
+    kernarg segment uses) and launched in one library call.  Out-of-range values raise
+    instead of wrapping."""
+
+    __slots__ = ("handle", "name", "argtypes", "block", "lds", "_packer")
 
     def __init__(self, handle: int, name: str, argtypes: tuple, block: int, lds: int = 0):
         self.handle, self.name, self.argtypes, self.block, self.lds = handle, name, argtypes, block, lds
+        try:
+            self._packer = struct.Struct("@" + "".join(_ARG_CODES[t] for t in argtypes))
+        except KeyError as error:
+            raise TypeError(f"{name}: unsupported kernel argument type {error}") from None
 
     def launch(self, grid, args, stream: int) -> None:
         if len(args) != len(self.argtypes):
             raise TypeError(f"{self.name}: expected {len(self.argtypes)} arguments, got {len(args)}")
-        values = [t(a) for t, a in zip(self.argtypes, args)]
-        ptrs = (ctypes.c_void_p * len(values))(*[ctypes.addressof(v) for v in values])
-        g = (ctypes.c_uint32 * 3)(*(tuple(int(d) for d in grid) + (1, 1, 1))[:3])
-        b = (ctypes.c_uint32 * 3)(self.block, 1, 1)
-        rc = _lib.nep_launch(self.handle, g, b, self.lds, ctypes.c_void_p(stream), ptrs, len(values))
-        _check(rc, f"launch {self.name}")
+        try:
+            image = self._packer.pack(*args)
+        except struct.error as error:
+            raise ValueError(f"{self.name}: kernel argument out of range ({error})") from None
+        gx = int(grid[0])
+        gy = int(grid[1]) if len(grid) > 1 else 1
+        gz = int(grid[2]) if len(grid) > 2 else 1
+        rc = _lib.nep_launch_packed(self.handle, gx, gy, gz, self.block, self.lds, stream,
+                                    image, len(image))
+        if rc != NEP_OK:
+            _check(rc, f"launch {self.name}")
 
 
 class Program:
@@ -190,6 +213,10 @@ class Program:
 
 
 def current_stream(device) -> int:
+    """Raw hipStream_t of torch's current stream on `device` (a torch.device or index)."""
     import torch
 
-    return torch.cuda.current_stream(device).cuda_stream
+    index = device.index if isinstance(device, torch.device) else device
+    if index is None:
+        index = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)

@@ -23,7 +23,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(hip.EXPORTED), names
     for name in names:
         assert getattr(lib, name) is not None
-    assert lib.nep_abi_version() == 1
+    assert lib.nep_abi_version() == 2
 
 
 def test_compile_code_object_and_error_reporting():
