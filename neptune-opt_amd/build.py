@@ -1,7 +1,8 @@
 """Build step of the neptune HIP backend (no GPU needed).
 
 1. hipcc builds the C-ABI runtime libneptune_hip.so (host code: hiprtc + module launch) in
-   place, next to the Python package, so that it travels with the source tree.
+   place, next to the Python package, so that it travels with the source tree; g++ builds
+   the operators' C++ dispatcher kernels (_neptune_dispatch.so) beside it.
 2. Every generated kernel unit the benchmark configurations and tests use is compiled with
    hiprtc for gfx950 into the on-disk code-object cache (neptune_codegen/_codeobj).  That both
    proves each emitted unit compiles and spares the GPU host the compile.
@@ -17,6 +18,8 @@ ROOT = pathlib.Path(__file__).resolve().parent
 REPO = ROOT.parent
 LIB = ROOT / "neptune_codegen" / "_lib" / "libneptune_hip.so"
 SRC = ROOT / "csrc" / "nep_runtime.cpp"
+DISPATCH = ROOT / "neptune_codegen" / "_lib" / "_neptune_dispatch.so"
+DISPATCH_SRC = ROOT / "csrc" / "nep_dispatch.cpp"
 
 
 def build_library(verbose: bool = True) -> pathlib.Path:
@@ -32,6 +35,33 @@ def build_library(verbose: bool = True) -> pathlib.Path:
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
     return LIB
+
+
+def build_dispatch(verbose: bool = True) -> pathlib.Path:
+    """g++: the C++ dispatcher kernels (host code only) against torch's headers and
+    libraries and libneptune_hip.so, as an importable extension module next to it."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = cpp_extension.library_paths()[0]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = DISPATCH.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-fPIC", "-shared", "-std=c++17",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-DTORCH_EXTENSION_NAME=_neptune_dispatch", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           *(f"-I{p}" for p in cpp_extension.include_paths()),
+           f"-I{sysconfig.get_paths()['include']}", "-I/opt/rocm/include",
+           f"-I{REPO / 'include'}", str(DISPATCH_SRC), "-o", str(tmp),
+           f"-L{torch_lib}", f"-L{LIB.parent}", "-lneptune_hip", "-lc10", "-lc10_hip",
+           "-ltorch", "-ltorch_cpu", "-ltorch_python",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
+    if verbose:
+        print("[build]", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, DISPATCH)
+    return DISPATCH
 
 
 def precompile(verbose: bool = True) -> int:
@@ -50,6 +80,7 @@ def precompile(verbose: bool = True) -> int:
 
 def main() -> None:
     build_library()
+    build_dispatch()
     precompile()
 
 

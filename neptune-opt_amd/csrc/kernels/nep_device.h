@@ -31,6 +31,15 @@ __device__ __forceinline__ bool is_finite(float v) { return __builtin_isfinite(v
 // the fold terms where the reference's Triton lowering also uses an approximate exponential.
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
+// num / den for a denominator shared by many numerators (a fold term's per-tile producer
+// value): one IEEE division 1/den that the compiler shares across the unrolled elements, then
+// a multiply per element (<= 1.5 ulp from the quotient).  A denominator below 2^-64 is first
+// scaled by the exact power of two 2^64 on both sides, so 1/den stays finite for denormals.
+__device__ __forceinline__ float quot(float num, float den) {
+  const float sc = __builtin_fabsf(den) < 0x1p-64f ? 0x1p64f : 1.0f;
+  return (num * sc) * (1.0f / (den * sc));
+}
+
 // ---------------------------------------------------------------- storage dtypes
 // bf16 -> fp32 is exact (the high half of an fp32 pattern).  fp32 -> bf16 rounds to nearest
 // even.  f32_to_bf16_bits is the integer statement of that rounding (NaN -> the canonical

@@ -531,17 +531,35 @@ __device__ __forceinline__ void fold_two_pass(const typename St::T* __restrict__
   const i64 c1 = live ? ncols : 0;
   const float n = (float)ncols;
   const int wave = threadIdx.x >> 6, first = (wave / RC::WPR) * RC::WPR;
+  // A row that fits in one tile stays in registers: pass 2 reads what pass 1 loaded, so the
+  // row crosses HBM once (same values, same order as reading it twice).
+  const bool resident = ncols <= TL::TILE;
+  float keep[TL::K];
+  bool kept[UNROLL];
   // pass 1: the producer
   float m = F::kProducerSum ? 0.0f : -kInf;
-  for (i64 tile = 0; tile < c1; tile += TL::TILE) {
-    float v[TL::K];
+  if (resident) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      if (!TL::load_slot(rp, stride_col, tile, c1, t, u, v)) continue;
+      kept[u] = TL::load_slot(rp, stride_col, 0, c1, t, u, keep);
+      if (!kept[u]) continue;
 #pragma unroll
       for (int j = 0; j < TL::VEC; ++j) {
-        const float o = F::phi(v[u * TL::VEC + j], n);
+        const float o = F::phi(keep[u * TL::VEC + j], n);
         m = F::kProducerSum ? (m + o) : __builtin_fmaxf(m, o);
+      }
+    }
+  } else {
+    for (i64 tile = 0; tile < c1; tile += TL::TILE) {
+      float v[TL::K];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        if (!TL::load_slot(rp, stride_col, tile, c1, t, u, v)) continue;
+#pragma unroll
+        for (int j = 0; j < TL::VEC; ++j) {
+          const float o = F::phi(v[u * TL::VEC + j], n);
+          m = F::kProducerSum ? (m + o) : __builtin_fmaxf(m, o);
+        }
       }
     }
   }
@@ -558,15 +576,27 @@ __device__ __forceinline__ void fold_two_pass(const typename St::T* __restrict__
   }
   // pass 2: the term at the final producer value
   float acc = consumer_init<F>();
-  for (i64 tile = 0; tile < c1; tile += TL::TILE) {
-    float v[TL::K];
+  if (resident) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      if (!TL::load_slot(rp, stride_col, tile, c1, t, u, v)) continue;
+      if (!kept[u]) continue;
 #pragma unroll
       for (int j = 0; j < TL::VEC; ++j) {
-        const float tv = F::term(v[u * TL::VEC + j], m, n);
+        const float tv = F::term(keep[u * TL::VEC + j], m, n);
         acc = F::kConsumerMax ? __builtin_fmaxf(acc, tv) : (acc + tv);
+      }
+    }
+  } else {
+    for (i64 tile = 0; tile < c1; tile += TL::TILE) {
+      float v[TL::K];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        if (!TL::load_slot(rp, stride_col, tile, c1, t, u, v)) continue;
+#pragma unroll
+        for (int j = 0; j < TL::VEC; ++j) {
+          const float tv = F::term(v[u * TL::VEC + j], m, n);
+          acc = F::kConsumerMax ? __builtin_fmaxf(acc, tv) : (acc + tv);
+        }
       }
     }
   }

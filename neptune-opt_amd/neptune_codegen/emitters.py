@@ -155,16 +155,17 @@ def emit_fold_policy(sk: Skeleton, values: dict | None = None, *, struct_name: s
     check_supported(sk)
     bind = param_bindings(sk, values)
     floor = (not sk.two_pass) and coordinate_needs_floor(sk)
-    phi = to_hip(producer_operand_expr(sk), {**bind, c_sym: "v"})
+    phi = to_hip(producer_operand_expr(sk), {**bind, c_sym: "v"}, shared=c_sym)
     if sk.two_pass:
-        term = to_hip(term_expr(sk), {**bind, c_sym: "v", s2_sym: "den"})
+        term = to_hip(term_expr(sk), {**bind, c_sym: "v", s2_sym: "den"}, shared=c_sym)
         rho, beta, has_bias = "1.0f", "0.0f", False
         fin_m = "m"
     else:
         if sk.is_log:
             term = f"nep::fast_exp({phi} - den)"
         else:
-            term = to_hip(_marked(term_expr(sk)), {**bind, c_sym: "v", s2_sym: "den"})
+            term = to_hip(_marked(term_expr(sk)), {**bind, c_sym: "v", s2_sym: "den"},
+                          shared=c_sym)
         a, b = repair_factor(sk), repair_bias(sk)
         rho = to_hip(_marked(a), {**bind, s_sym: "q", s2_sym: "q2"})
         has_bias = b != 0

@@ -155,14 +155,19 @@ class Kernel:
     kernarg segment uses) and launched in one library call.  Out-of-range values raise
     instead of wrapping."""
 
-    __slots__ = ("handle", "name", "argtypes", "block", "lds", "_packer")
+    __slots__ = ("handle", "name", "argtypes", "block", "lds", "_packer", "pointer_offsets")
 
     def __init__(self, handle: int, name: str, argtypes: tuple, block: int, lds: int = 0):
         self.handle, self.name, self.argtypes, self.block, self.lds = handle, name, argtypes, block, lds
         try:
-            self._packer = struct.Struct("@" + "".join(_ARG_CODES[t] for t in argtypes))
+            codes = "".join(_ARG_CODES[t] for t in argtypes)
         except KeyError as error:
             raise TypeError(f"{name}: unsupported kernel argument type {error}") from None
+        self._packer = struct.Struct("@" + codes)
+        # byte offset of every pointer argument in the image, by argument index
+        self.pointer_offsets = {
+            i: struct.calcsize("@" + codes[:i + 1]) - struct.calcsize("@P")
+            for i, c in enumerate(codes) if c == "P"}
 
     def launch(self, grid, args, stream: int) -> None:
         if len(args) != len(self.argtypes):
@@ -178,6 +183,41 @@ class Kernel:
                                     image, len(image))
         if rc != NEP_OK:
             _check(rc, f"launch {self.name}")
+        recorder = getattr(_recording, "active", None)
+        if recorder is not None:
+            recorder.launches.append((self, (gx, gy, gz), image, tuple(args)))
+
+
+class Recorder:
+    """What one operator body launched (kernel, grid, image, arguments) and which scratch
+    tensors it allocated for those launches; see `recording`."""
+
+    def __init__(self):
+        self.launches: list = []
+        self.buffers: list = []
+
+
+_recording = threading.local()
+
+
+class recording:
+    """Context manager: record every Kernel.launch and `scratch` allocation on this thread."""
+
+    def __enter__(self) -> Recorder:
+        self._previous = getattr(_recording, "active", None)
+        _recording.active = Recorder()
+        return _recording.active
+
+    def __exit__(self, *exc) -> None:
+        _recording.active = self._previous
+
+
+def scratch(tensor):
+    """Mark a tensor allocated by a launch path as per-call scratch (recorded when active)."""
+    recorder = getattr(_recording, "active", None)
+    if recorder is not None:
+        recorder.buffers.append(tensor)
+    return tensor
 
 
 class Program:

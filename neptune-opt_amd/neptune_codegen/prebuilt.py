@@ -21,6 +21,14 @@ def _fold_programs():
         block, warps = best_config(rows, ncols, dtype, None, device_name="gfx950")
         var = _fold_variant(x2, ncols, block, warps)
         out.append(compile_skeleton("logsumexp", lse).program(var))
+    from neptune_codegen.skeleton import supported
+
+    x2 = torch.empty((16384, 4096), device="meta", dtype=torch.float32)
+    block, warps = best_config(16384, 4096, torch.float32, None, device_name="gfx950")
+    for name in supported():
+        params = {**param_defaults(name), **({"eps": 1e-6} if name == "rmsnorm_max" else {})}
+        prog = compile_skeleton(name, params)
+        out.append(prog.program(_fold_variant(x2, 4096, block, warps, resident=prog.sk.two_pass)))
     x2 = torch.empty((64, 262144), device="meta", dtype=torch.bfloat16)
     partial, _merge = compile_skeleton("logsumexp", lse, plan="split")
     out.append(partial.program(_fold_variant(x2, 262144, 1024, 4, split_block=1024)))

@@ -5,8 +5,11 @@ lowering rules that carry numerical meaning are kept:
 
   * exp is a true exponential, never clipped (a clipped exp breaks the repair cocycle);
     it lowers to nep::fast_exp, 2^(x log2 e) on the hardware exp2;
-  * tanh(x) lowers to 2*sigmoid(2x) - 1, saturating to +-1 instead of overflowing;
+  * tanh(x) lowers to 2*sigmoid(2x) - 1 with the hardware reciprocal (v_rcp_f32, 1 ulp),
+    saturating to +-1 instead of overflowing;
   * a marked quotient power _Q(a, b, k) lowers to k products of (a / b), never a**k / b**k;
+  * with `shared` given, a quotient whose denominator does not mention that symbol (a fold
+    term's divisor fixed per tile) lowers to nep::quot, a multiply by one shared reciprocal;
   * x**(1/2) is sqrtf(x), x**(-1/2) is 1.0f / sqrtf(x), integer powers are products;
   * other fractional powers are allowed only for a provably positive base (exp2(log2(b) p));
   * numeric literals are rounded to fp32 once and written as exact hex-float literals.
@@ -44,9 +47,15 @@ def _positive_base(base: sp.Expr) -> bool:
     return base.is_positive is True
 
 
-def to_hip(expr: sp.Expr, names: dict) -> str:
-    """Render `expr` as an fp32 C++ expression; `names` maps symbols to source text."""
+def to_hip(expr: sp.Expr, names: dict, shared: sp.Symbol | None = None) -> str:
+    """Render `expr` as an fp32 C++ expression; `names` maps symbols to source text.  With
+    `shared` (the per-element symbol), divisors free of it become shared reciprocals."""
     expr = sp.sympify(expr)
+
+    def divide(top: str, bottom: str, divisor: sp.Expr) -> str:
+        if shared is not None and not divisor.has(shared):
+            return f"nep::quot({top}, {bottom})"
+        return f"({top} / {bottom})"
 
     def rec(e: sp.Expr) -> str:
         if isinstance(e, _Q):
@@ -54,7 +63,7 @@ def to_hip(expr: sp.Expr, names: dict) -> str:
             k = int(k)
             if k <= 0:
                 raise TranslationError(f"quotient power needs a positive integer exponent: {e}")
-            q = f"({rec(num)} / {rec(den)})"
+            q = divide(rec(num), rec(den), den)
             return "(" + " * ".join([q] * k) + ")"
         if e.is_Symbol:
             if e not in names:
@@ -72,17 +81,18 @@ def to_hip(expr: sp.Expr, names: dict) -> str:
             coeff, rest = e.as_coeff_Mul()
             if coeff == -1:
                 return f"(-{rec(rest)})"
-            numer, denom = [], []
+            numer, denom, divisor = [], [], sp.Integer(1)
             for factor in e.args:
                 base, ex = factor.as_base_exp()
                 if ex.is_Number and ex.is_negative:
                     denom.append(rec(base ** (-ex)))
+                    divisor = divisor * base ** (-ex)
                 else:
                     numer.append(rec(factor))
             top = " * ".join(numer) if numer else "1.0f"
             if not denom:
                 return f"({top})"
-            return f"({top} / ({' * '.join(denom)}))"
+            return divide(f"({top})", f"({' * '.join(denom)})", divisor)
         if e.is_Pow:
             base, ex = e.args
             if ex.is_Integer:
@@ -91,7 +101,7 @@ def to_hip(expr: sp.Expr, names: dict) -> str:
                     return "1.0f"
                 b = rec(base)
                 prod = "(" + " * ".join([b] * abs(k)) + ")"
-                return prod if k > 0 else f"(1.0f / {prod})"
+                return prod if k > 0 else divide("1.0f", prod, base)
             if ex == sp.Rational(1, 2):
                 return f"sqrtf({rec(base)})"
             if ex == sp.Rational(-1, 2):
@@ -107,7 +117,7 @@ def to_hip(expr: sp.Expr, names: dict) -> str:
             return f"logf({rec(e.args[0])})"
         if isinstance(e, sp.tanh):
             x = rec(e.args[0])
-            return f"(2.0f / (1.0f + nep::fast_exp(-2.0f * {x})) - 1.0f)"
+            return f"(2.0f * __builtin_amdgcn_rcpf(1.0f + nep::fast_exp(-2.0f * {x})) - 1.0f)"
         if isinstance(e, sp.Abs):
             return f"fabsf({rec(e.args[0])})"
         if isinstance(e, (sp.Max, sp.Min)):

@@ -14,7 +14,7 @@ import math
 import threading
 
 from neptune_codegen import hip
-from neptune_codegen.autotune import (MAX_UNROLL, UNROLL, best_config, lanes_per_row,
+from neptune_codegen.autotune import (MAX_TPR, MAX_UNROLL, UNROLL, best_config, lanes_per_row,
                                       parameter_identity, parameter_tag, vec_of)
 from neptune_codegen.emitters import (BASE_OPTIONS, NO_CONTRACT, FoldVariant, RowVariant,
                                       check_supported, emit_kernel_source, emit_rms_state_source,
@@ -146,10 +146,13 @@ def _is_vector(x2, ncols: int, vec: int, extra_align: int = 0) -> bool:
             and x2.data_ptr() % 16 == 0 and (extra_align == 0 or extra_align % vec == 0))
 
 
-def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: int = 0) -> FoldVariant:
+def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: int = 0,
+                  resident: bool = False) -> FoldVariant:
     """Launch shape: 16-byte loads when the layout allows, lanes per row from BLOCK (a tile
     wider than the workgroup's lanes gives each lane up to MAX_UNROLL slots first), workgroup =
-    max(64 * num_warps, lanes per row)."""
+    max(64 * num_warps, lanes per row).  `resident` (two-pass folds) widens the tile, slots
+    per lane first and then lanes, until one tile holds the whole row where that fits
+    (MAX_UNROLL slots of MAX_TPR lanes): the second pass then reads registers, not HBM."""
     vec = vec_of(x2.dtype)
     vector = _is_vector(x2, ncols, vec, split_block)
     if vector and split_block and split_block < vec:
@@ -161,6 +164,12 @@ def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: in
     while tpr > 64 * waves and unroll < MAX_UNROLL and not split_block:
         tpr //= 2
         unroll *= 2
+    if resident and not split_block:
+        per_slot = vec if vector else 1
+        while tpr * unroll * per_slot < ncols and unroll < MAX_UNROLL:
+            unroll *= 2
+        while tpr * unroll * per_slot < ncols and tpr < MAX_TPR:
+            tpr *= 2
     return FoldVariant(str(x2.dtype).replace("torch.", ""), vector, tpr, unroll, waves)
 
 
@@ -176,17 +185,17 @@ def launch_reduction(kernel, plan, x2, out, rows, ncols, block, num_warps, *, wr
     device = x2.device.index if x2.device.index is not None else torch.cuda.current_device()
     stream = hip.current_stream(x2.device)
     if plan == "serial":
-        var = _fold_variant(x2, ncols, block, num_warps)
+        var = _fold_variant(x2, ncols, block, num_warps, resident=kernel.sk.two_pass)
         k = kernel.kernel(var, "", device)
         rpw = max(1, var.wg // var.tpr)
         k.launch((_grid_1d(rows, rpw),),
                  (x2.data_ptr(), out.data_ptr(), rows, ncols, x2.stride(0), x2.stride(1)), stream)
         return
     nparts, _merge = split_launch_shape(ncols, block)
-    partial_m = torch.empty((rows, nparts), device=x2.device, dtype=torch.float32)
-    partial_a = torch.empty((rows, nparts), device=x2.device, dtype=torch.float32)
-    partial_v = torch.empty((rows, nparts), device=x2.device, dtype=torch.int32)
-    partial_s = torch.empty((rows, nparts), device=x2.device, dtype=torch.int32)
+    partial_m = hip.scratch(torch.empty((rows, nparts), device=x2.device, dtype=torch.float32))
+    partial_a = hip.scratch(torch.empty((rows, nparts), device=x2.device, dtype=torch.float32))
+    partial_v = hip.scratch(torch.empty((rows, nparts), device=x2.device, dtype=torch.int32))
+    partial_s = hip.scratch(torch.empty((rows, nparts), device=x2.device, dtype=torch.int32))
     partial, merge = kernel
     var = _fold_variant(x2, ncols, block, num_warps, split_block=block)
     kp = partial.kernel(var, "partial", device)
@@ -382,8 +391,8 @@ def launch_rms_norm(kernel, x, gamma, out, *, plan="serial", wrapper=None):
                   flat.stride(1), g_stride), stream)
         return
     parts, _ = split_launch_shape(width, 1024)
-    totals = torch.empty((rows, parts), device=x.device, dtype=torch.float32)
-    counts = torch.empty((rows, parts), device=x.device, dtype=torch.int64)
+    totals = hip.scratch(torch.empty((rows, parts), device=x.device, dtype=torch.float32))
+    counts = hip.scratch(torch.empty((rows, parts), device=x.device, dtype=torch.int64))
     var = _row_variant(flat, gamma, width, tile=1024)
     kp, km = kernel.kernels(var, device)
     rpw = max(1, var.wg // var.tpr)

@@ -5,13 +5,15 @@ Mirrors the reference's neptune_codegen/torch_op.py: op naming from `autotune.op
 :145-190), and the whole segment backend -- parameter validation, span construction with
 device-side asserts, metadata contract, launch and op registration (:208-466).  Ops are
 registered with torch.library.custom_op (schema identical to the reference's triton_op) and
-a metadata-only fake; their bodies launch generated HIP kernels through libneptune_hip.
+a metadata-only fake; their bodies launch generated HIP kernels through libneptune_hip.  The
+row-fold and RMS / L2 operators also get C++ dispatcher kernels that replay a recorded launch
+plan per input layout (neptune_codegen.dispatch).
 """
 from __future__ import annotations
 
 import threading
 
-from neptune_codegen import autotune, hip
+from neptune_codegen import autotune, dispatch, hip
 from neptune_codegen.emitters import (BASE_OPTIONS, NO_CONTRACT, SegmentVariant,
                                       emit_segment_source, segment_kernel_name)
 from neptune_codegen.skeleton import param_defaults
@@ -75,6 +77,7 @@ def as_triton_op(name: str, block: int | None = None, num_warps: int | None = No
         return torch.empty(x.shape[:-1] + ((1,) if keepdim else ()), device=x.device, dtype=x.dtype)
 
     op = _register(key, "(Tensor x) -> Tensor", _impl, _fake)
+    dispatch.install(key, 1, _impl)
     op.__name__ = f"{lib}_{impl_name}"
     with _lock:
         _TRITON_OPS[key] = op
@@ -160,6 +163,7 @@ def as_state_op(name, params=None, plan="serial", lib="neptune"):
 
         schema = "(Tensor x) -> Tensor"
     op = _register(f"{lib}::{impl_name}", schema, _impl, _fake)
+    dispatch.install(f"{lib}::{impl_name}", 2 if name == "rms_norm" else 1, _impl)
     op.__name__ = f"{lib}_{impl_name}"
     with _lock:
         _STATE_OPS[key] = op

@@ -213,15 +213,100 @@ def rewrite_match(gm, match, *, lib="neptune", plan="serial"):
     gm.meta["neptune_replaced_roots"] = renamed
     root.replace_all_uses_with(call)
     graph.erase_node(root)
-    # only dead, pure nodes of this region go; shared values and side effects stay
+    # only dead, pure nodes of this region go; shared values and side effects stay.  An
+    # export-time metadata assert on a region-internal value is the one side effect dropped
+    # with it: the value is no longer computed, so there is nothing left to check.
     for node in reversed(match.region_nodes):
         if node is root or node.op in ("placeholder", "output", "get_attr"):
             continue
+        checks = [u for u in node.users if _is_metadata_assert(u)]
+        if checks and len(checks) == len(node.users):
+            for check in checks:
+                graph.erase_node(check)
         if not node.users and not node.is_impure():
             graph.erase_node(node)
+    if getattr(match, "kind", "scalar") != "structured":
+        call = _absorb_casts(gm, call, match, keepdim, lib, plan)
     graph.lint()
     gm.recompile()
     return call, None
+
+
+def _is_metadata_assert(node) -> bool:
+    import torch
+
+    return (node.op == "call_function" and not node.users
+            and node.target is torch.ops.aten._assert_tensor_metadata.default)
+
+
+def _dtype_cast(node, source=None):
+    """The dtype of `node` when it is a pure dtype conversion of `source` (aten._to_copy with
+    only dtype=, or aten.to.dtype with default non_blocking/copy/memory_format)."""
+    import torch
+
+    if node.op != "call_function":
+        return None
+    if node.target is torch.ops.aten._to_copy.default:
+        if len(node.args) != 1 or set(node.kwargs) != {"dtype"}:
+            return None
+        dtype = node.kwargs["dtype"]
+    elif node.target is torch.ops.aten.to.dtype:
+        if len(node.args) != 2 or any(node.kwargs.get(k) not in (None, False)
+                                      for k in ("non_blocking", "copy", "memory_format")):
+            return None
+        if set(node.kwargs) - {"non_blocking", "copy", "memory_format"}:
+            return None
+        dtype = node.args[1]
+    else:
+        return None
+    if source is not None and node.args[0] is not source:
+        return None
+    return dtype
+
+
+def _absorb_casts(gm, call, match, keepdim, lib, plan):
+    """fold(_to_copy(x, float32)) read only through _to_copy(., x.dtype), x 16-bit, becomes
+    fold(x): the fold kernels widen 16-bit loads to fp32 exactly, accumulate in fp32 and round
+    once to the input dtype on store -- the cast pair's arithmetic without the fp32 copy of x
+    in HBM (compound lowering inserts that pair, lowering.py's accumulation casts)."""
+    import torch
+
+    widen = call.args[0]
+    if _dtype_cast(widen) is not torch.float32:
+        return call
+    source = widen.args[0]
+    value = _tensor_value(source)
+    if value is None or value.dtype not in (torch.bfloat16, torch.float16):
+        return call
+    checks = [u for u in call.users if _is_metadata_assert(u)]
+    users = [u for u in call.users if u not in checks]
+    if len(users) != 1 or _dtype_cast(users[0], call) is not value.dtype:
+        return call
+    narrow = users[0]
+    block, warps = _launch_config(source)
+    if plan == "split":
+        block, warps = 1024, 4
+    params = {**CG.param_defaults(match.skeleton), **match.params}
+    op = CG.op_handle(match.skeleton, params=params, lib=lib, keepdim=keepdim, block=block,
+                      num_warps=warps, plan=plan)
+    graph = gm.graph
+    with graph.inserting_before(narrow):
+        fused = graph.call_function(op, args=(source,))
+    fused.meta = copy.copy(narrow.meta)
+    renamed = copy.deepcopy(gm.meta.get("neptune_replaced_roots", {}))
+    for old, new in list(renamed.items()):
+        if new == call.name:
+            renamed[old] = fused.name
+    renamed[narrow.name] = fused.name
+    gm.meta["neptune_replaced_roots"] = renamed
+    narrow.replace_all_uses_with(fused)
+    graph.erase_node(narrow)
+    for check in checks:            # asserted the fp32 value, which is no longer computed
+        graph.erase_node(check)
+    graph.erase_node(call)
+    if not widen.users:
+        graph.erase_node(widen)
+    return fused
 
 
 def rewrite(gm, values=None, ops=None, lib="neptune", *, plan="serial"):

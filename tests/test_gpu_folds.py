@@ -94,6 +94,33 @@ def test_every_skeleton_every_dtype(name, dtype, plan):
             torch.testing.assert_close(got.cpu().float(), want, rtol=torch.finfo(dtype).eps, atol=1e-5)
 
 
+@pytest.mark.parametrize("name", ["stable_l2", "linear_attn", "sumsq_div", "decay_renorm",
+                                  "rmsnorm_max", "variance"])
+def test_quotient_terms_at_extreme_magnitudes(name):
+    """Terms divide by a per-tile producer value through one shared reciprocal; rows whose
+    magnitudes are denormal (divisor < 2^-126), tiny, or huge must still match the oracle."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(11)
+    params = {"eps": 1e-6} if name == "rmsnorm_max" else {}
+    for scale in (1e-39, 1e-30, 3e-20, 1.0, 1e18, 1e30):
+        if name == "rmsnorm_max" and scale > 1e19:
+            # x^2 overflows: the running mean is inf on both sides of a merge and the repair
+            # sqrt(eps + s)/sqrt(eps + s2) is inf/inf = NaN, in the reference's algebra too
+            # (its Triton repair is the same ratio); the closed form says 0.
+            continue
+        x = torch.rand(8, 700, generator=g) + 0.05
+        x = (x * scale).float()
+        _say(f"quotient fold {name} scale {scale:g}")
+        got = CG.run(name, x.to(dev), **params).cpu()
+        want = R.reference(name, x, **params)
+        ok = torch.isfinite(want)
+        assert torch.equal(torch.isfinite(got), ok), (name, scale)
+        # results in the denormal range carry fewer significant bits than fp32's 24: there
+        # the bound is absolute, one smallest normal
+        torch.testing.assert_close(got[ok], want[ok], rtol=R.summation_tolerance(torch.float32, 700),
+                                   atol=torch.finfo(torch.float32).tiny)
+
+
 def test_strided_views_and_keepdim():
     dev = _dev()
     g = torch.Generator().manual_seed(3)

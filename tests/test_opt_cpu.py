@@ -152,3 +152,108 @@ def test_compile_best_validates_before_touching_a_device():
     if not torch.cuda.is_available():
         with pytest.raises(RuntimeError, match="GPU"):
             neptune_opt.compile_best(Model(), (X,))
+
+
+@torch.library.custom_op("neptune_cpu_standin::rms", mutates_args=())
+def _rms(x: torch.Tensor, gamma: torch.Tensor) -> torch.Tensor:
+    z = x.float()
+    return (z * torch.rsqrt(z.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype) * gamma
+
+
+@_rms.register_fake
+def _(x, gamma):
+    return x.new_empty(x.shape)
+
+
+class LSE(torch.nn.Module):
+    def forward(self, x):
+        return torch.logsumexp(x, dim=-1)
+
+
+class UpcastLSE(torch.nn.Module):
+    def forward(self, x):
+        return torch.logsumexp(x.float(), dim=-1)
+
+
+class RMS(torch.nn.Module):
+    def __init__(self, width):
+        super().__init__()
+        g = torch.Generator().manual_seed(3)
+        self.gamma = torch.nn.Parameter((1 + 0.1 * torch.randn(width, generator=g)).bfloat16(),
+                                        requires_grad=False)
+
+    def forward(self, x):
+        z = x.to(torch.float32)
+        return (z * torch.rsqrt(z.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype) * self.gamma
+
+
+def _calls(ep):
+    return [n for n in ep.graph_module.graph.nodes if n.op == "call_function"]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_compound_lowering_casts_are_absorbed_into_the_fold(dtype):
+    """logsumexp on a 16-bit input lowers to upcast -> fold -> downcast; the rewrite feeds the
+    16-bit tensor to the fold directly (one call, no fp32 copy of the input)."""
+    x = (3 * torch.randn(16, 64, generator=torch.Generator().manual_seed(4))).to(dtype)
+    model = LSE().eval()
+    ep = torch.export.export(model, (x,))
+    a, b = _standin(_lse._opoverload)
+    with a, b:
+        report = neptune_opt.apply(ep, verify_with=(model, (x,)), max_ulps=2)
+    assert report.fusions and report.verified is True, report.summary()
+    calls = _calls(ep)
+    assert [n.target for n in calls] == [_lse._opoverload]
+    assert calls[0].args[0].op == "placeholder"
+    out = ep.module()(x)
+    assert out.dtype == dtype and out.shape == (16,)
+
+
+def test_explicit_upcast_keeps_the_fp32_result():
+    x = torch.randn(16, 64, generator=torch.Generator().manual_seed(5)).bfloat16()
+    model = UpcastLSE().eval()
+    ep = torch.export.export(model, (x,))
+    a, b = _standin(_lse._opoverload)
+    with a, b:
+        report = neptune_opt.apply(ep, verify_with=(model, (x,)))
+    assert report.fusions, report.summary()
+    targets = [n.target for n in _calls(ep)]
+    assert _lse._opoverload in targets and torch.ops.aten.to.dtype in targets
+    assert ep.module()(x).dtype == torch.float32
+
+
+class RoundTripLSE(torch.nn.Module):
+    def forward(self, x):
+        return torch.logsumexp(x.float(), dim=-1).to(x.dtype)
+
+
+def test_user_written_cast_pair_is_absorbed_too():
+    x = torch.randn(16, 64, generator=torch.Generator().manual_seed(7)).half()
+    model = RoundTripLSE().eval()
+    ep = torch.export.export(model, (x,))
+    a, b = _standin(_lse._opoverload)
+    with a, b:
+        report = neptune_opt.apply(ep, verify_with=(model, (x,)), max_ulps=2)
+    assert report.fusions and report.verified is True, report.summary()
+    fused = [n for n in _calls(ep) if n.target is _lse._opoverload]
+    assert len(fused) == 1 and fused[0].args[0].op == "placeholder"
+    assert ep.module()(x).dtype == torch.float16
+
+
+def test_metadata_asserts_do_not_keep_a_fused_region_alive():
+    """export records a dtype assert on the region-internal `.to(x.dtype)` value; after the
+    rewrite neither it nor the region's arithmetic may remain (the input's assert stays)."""
+    x = torch.randn(32, 64, generator=torch.Generator().manual_seed(6)).bfloat16()
+    model = RMS(64).eval()
+    ep = torch.export.export(model, (x,))
+    with patch("neptune_codegen.state_op_handle", lambda *a, **k: _rms._opoverload):
+        report = neptune_opt.apply(ep, verify_with=(model, (x,)), capabilities=("rms_norm",),
+                                   max_ulps=2)
+    assert report.fusions and report.verified is True, report.summary()
+    targets = [n.target for n in _calls(ep)]
+    assert _rms._opoverload in targets
+    leftover = [t for t in targets if t not in (_rms._opoverload,
+                                                 torch.ops.aten._assert_tensor_metadata.default)]
+    assert leftover == [], leftover
+    asserts = [n for n in _calls(ep) if n.target is torch.ops.aten._assert_tensor_metadata.default]
+    assert all(n.args[0].op == "placeholder" for n in asserts)
