@@ -168,8 +168,8 @@ __device__ __forceinline__ void exact_tile(State& s, const typename St::T* row, 
   bool ok[UNROLL];
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) ok[u] = TL::load_slot(row, stride_col, tile, c1, t, u, v);
-  State c;
   if constexpr (F::kLog) {
+    State c;
     int status = 0, seen = 0;
     float m = -kInf;
 #pragma unroll
@@ -201,9 +201,14 @@ __device__ __forceinline__ void exact_tile(State& s, const typename St::T* row, 
     c.acc = acc;
     c.seen = seen;
     c.status = status;
+    s = merge_state<F>(s, c);
   } else {
+    // Streaming update (one repair per tile instead of merge_state's two): the tile's terms
+    // are taken at the combined producer value, and only the carried accumulator is
+    // transported, acc' = rho(s.m, m') * acc (+ beta).  In real arithmetic this equals
+    // merge_state(s, chunk), whose chunk term is transported by rho(m_tile, m') instead.
     bool any = false;
-    float m = F::kProducerSum ? 0.0f : -kInf;
+    float mt = F::kProducerSum ? 0.0f : -kInf;
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       if (!ok[u]) continue;
@@ -211,11 +216,14 @@ __device__ __forceinline__ void exact_tile(State& s, const typename St::T* row, 
 #pragma unroll
       for (int j = 0; j < TL::VEC; ++j) {
         const float o = F::phi(v[u * TL::VEC + j], n);
-        m = F::kProducerSum ? (m + o) : __builtin_fmaxf(m, o);
+        mt = F::kProducerSum ? (mt + o) : __builtin_fmaxf(mt, o);
       }
     }
-    m = any ? m : 0.0f;
-    const float den = eff<F>(m);
+    if (!any) return;
+    const bool carried = s.seen != 0;
+    const float m_new =
+        carried ? (F::kProducerSum ? (s.m + mt) : __builtin_fmaxf(s.m, mt)) : mt;
+    const float den = eff<F>(m_new);
     float acc = consumer_init<F>();
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
@@ -226,12 +234,16 @@ __device__ __forceinline__ void exact_tile(State& s, const typename St::T* row, 
         acc = F::kConsumerMax ? __builtin_fmaxf(acc, tv) : (acc + tv);
       }
     }
-    c.m = m;
-    c.acc = acc;
-    c.seen = any ? 1 : 0;
-    c.status = 0;
+    if (carried) {
+      const float q = eff<F>(s.m);
+      float moved = s.acc * F::rho(q, den);
+      if constexpr (F::kHasBias) moved += F::beta(q, den);
+      acc = F::kConsumerMax ? __builtin_fmaxf(moved, acc) : (moved + acc);
+    }
+    s.m = m_new;
+    s.acc = acc;
+    s.seen = 1;
   }
-  s = merge_state<F>(s, c);
 }
 
 // Exact state of the columns [c0, c1) of one row, complete in every lane of the row.
