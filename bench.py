@@ -158,6 +158,15 @@ def per_fold(dev, xs_dev):
         rows = 64 if w == "split" else 16384
         key = "cfg2_split_bf16_64x262144" if w == "split" else f"cfg2_logsumexp_bf16_16384x{w}"
         folds[key] = measure_fold(key, make, cfg2_bytes(w), rows)
+    # log_softmax readout of the cfg2 W=32000 rows: the fold plus a full-row write
+    x = xs_dev[32000]
+
+    def make_ls(n, x=x):
+        xs = [x] + [x.clone() for _ in range(n - 1)]
+        return [lambda y=y: CG.run_log_softmax(y) for y in xs]
+
+    folds["cfg2_log_softmax_bf16_16384x32000"] = measure_fold(
+        "cfg2 log_softmax W=32000", make_ls, 2 * 16384 * 32000 * 2, 16384)
     # cfg3: RMSNorm and L2-normalize bf16 [32768, 4096], seed 3
     g3 = seeded(3)
     x3 = torch.randn(32768, 4096, generator=g3).bfloat16().to(dev)

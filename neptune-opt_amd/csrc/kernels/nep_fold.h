@@ -318,7 +318,50 @@ __device__ __forceinline__ void load_raw(RawTile<St, UNROLL, VECTOR>& r,
 // Per element: one max, one fma for the base-2 exponent, one exp2, one add.  The exponent
 // p*log2e - m*log2e carries an absolute error of about |m| * 2^-23, which is relative to the
 // readout m + log(acc): the row result keeps ~1e-7 relative accuracy.
-template <class F, class St, int TPR, int UNROLL, bool VECTOR>
+//
+// CENTERED evaluates exp2((p - m) * log2e) instead: p - m is exact, so an element equal to the
+// row maximum contributes exactly 1 (one more VALU op per element).  The readout uses it, so
+// that a log-probability of 0 comes out as 0 rather than as the rounding residue of m*log2e.
+// Fold one raw tile into a lane's exponential state.
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, bool CENTERED>
+__device__ __forceinline__ void log_fold_tile(LogLane& s,
+                                              const RawTile<St, UNROLL, VECTOR>& cur, float n) {
+  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+  float p[TL::K];
+  float tm = -kInf;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    float v[TL::VEC];
+    if constexpr (VECTOR) St::unpack(cur.w[u], v);
+    else v[0] = cur.s[u];
+#pragma unroll
+    for (int j = 0; j < TL::VEC; ++j) {
+      const int k = u * TL::VEC + j;
+      p[k] = cur.ok[u] ? F::phi(v[j], n) : -kInf;
+      tm = __builtin_fmaxf(tm, p[k]);
+    }
+  }
+  const float mn = __builtin_fmaxf(s.m, tm);
+  if (mn == -kInf) {
+    // No finite or +inf value yet; a NaN would otherwise be skipped by the max.
+#pragma unroll
+    for (int k = 0; k < TL::K; ++k) s.flag |= is_nan(p[k]) ? 1 : 0;
+  } else {
+    const float ml = mn * kLog2e;
+    // |m| above ~2.3e38 overflows m*log2e: route the row to the exact (subtracting) path.
+    if (!is_finite(ml) && is_finite(mn)) s.flag = 1;
+    float a = s.acc * fast_exp(s.m - mn);
+#pragma unroll
+    for (int k = 0; k < TL::K; ++k) {
+      if constexpr (CENTERED) a += __builtin_amdgcn_exp2f((p[k] - mn) * kLog2e);
+      else a += __builtin_amdgcn_exp2f(__builtin_fmaf(p[k], kLog2e, -ml));
+    }
+    s.acc = a;
+    s.m = mn;
+  }
+}
+
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, bool CENTERED = false>
 __device__ __forceinline__ LogLane log_row_lane(const typename St::T* row, i64 stride_col,
                                                 i64 c0, i64 c1, int t, float n) {
   typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
@@ -333,35 +376,7 @@ __device__ __forceinline__ LogLane log_row_lane(const typename St::T* row, i64 s
     RawTile<St, UNROLL, VECTOR> nxt;
     const bool more = tile + TL::TILE < c1;
     if (more) load_raw<St, TPR, UNROLL, VECTOR>(nxt, row, stride_col, tile + TL::TILE, c1, t);
-    float p[TL::K];
-    float tm = -kInf;
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      float v[TL::VEC];
-      if constexpr (VECTOR) St::unpack(cur.w[u], v);
-      else v[0] = cur.s[u];
-#pragma unroll
-      for (int j = 0; j < TL::VEC; ++j) {
-        const int k = u * TL::VEC + j;
-        p[k] = cur.ok[u] ? F::phi(v[j], n) : -kInf;
-        tm = __builtin_fmaxf(tm, p[k]);
-      }
-    }
-    const float mn = __builtin_fmaxf(s.m, tm);
-    if (mn == -kInf) {
-      // No finite or +inf value yet; a NaN would otherwise be skipped by the max.
-#pragma unroll
-      for (int k = 0; k < TL::K; ++k) s.flag |= is_nan(p[k]) ? 1 : 0;
-    } else {
-      const float ml = mn * kLog2e;
-      // |m| above ~2.3e38 overflows m*log2e: route the row to the exact (subtracting) path.
-      if (!is_finite(ml) && is_finite(mn)) s.flag = 1;
-      float a = s.acc * fast_exp(s.m - mn);
-#pragma unroll
-      for (int k = 0; k < TL::K; ++k) a += __builtin_amdgcn_exp2f(__builtin_fmaf(p[k], kLog2e, -ml));
-      s.acc = a;
-      s.m = mn;
-    }
+    log_fold_tile<F, St, TPR, UNROLL, VECTOR, CENTERED>(s, cur, n);
     if (more) cur = nxt;
   }
   return s;
@@ -386,23 +401,15 @@ __device__ __forceinline__ LogLane log_row_combine(LogLane s, LogLane* lds) {
 // ---------------------------------------------------------------- kernel bodies
 // Serial plan: one output per row (template.py:41-54).  WG threads per workgroup, WG/TPR rows
 // per workgroup (one row when TPR >= WG).
-template <class F, class St, int TPR, int UNROLL, bool VECTOR, int WG>
-__device__ __forceinline__ void fold_serial(const typename St::T* __restrict__ x,
-                                            typename St::T* __restrict__ out, i64 rows,
-                                            i64 ncols, i64 stride_row, i64 stride_col) {
-  static_assert(WG % 64 == 0 && (TPR <= 64 || WG % TPR == 0), "bad row mapping");
-  constexpr int RPW = WG / TPR;  // rows per workgroup
-  __shared__ State lds_state[WG / 64];
-  __shared__ LogLane lds_lane[WG / 64];
-  const int t = threadIdx.x % TPR;
-  const i64 row = (i64)blockIdx.x * RPW + threadIdx.x / TPR;
-  const bool live = row < rows;
-  const typename St::T* rp = x + (live ? row : 0) * stride_row;
-  const i64 c1 = live ? ncols : 0;
-  const float n = (float)ncols;
+// The row's fp32 result in every lane of the row (fast exponential path with the exact
+// fallback for NaN/+inf rows, or the exact state for other folds).  Every thread of the
+// workgroup must call it (it synchronises when a row spans several wavefronts).
+template <class F, class St, int TPR, int UNROLL, bool VECTOR>
+__device__ __forceinline__ float log_row_finish(LogLane s, const typename St::T* rp,
+                                                i64 stride_col, i64 c1, int t, float n,
+                                                State* lds_state, LogLane* lds_lane) {
   float result;
-  if constexpr (F::kLog) {
-    LogLane s = log_row_lane<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, 0, c1, t, n);
+  {
     s = log_row_combine<F, TPR>(s, lds_lane);
     const bool bad = s.flag != 0 || is_nan(s.acc);
     // Rows with NaN/+inf take the exact reference path; `bad` is uniform across the row.
@@ -419,12 +426,117 @@ __device__ __forceinline__ void fold_serial(const typename St::T* __restrict__ x
       if (bad) result = finalize_state<F>(e, n);
     }
     if (!bad) result = (s.m == -kInf) ? -kInf : F::finalize(s.m, s.acc, n);
+  }
+  return result;
+}
+
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, bool CENTERED = false>
+__device__ __forceinline__ float row_result(const typename St::T* rp, i64 stride_col, i64 c1,
+                                            int t, float n, State* lds_state,
+                                            LogLane* lds_lane) {
+  if constexpr (F::kLog) {
+    const LogLane s =
+        log_row_lane<F, St, TPR, UNROLL, VECTOR, CENTERED>(rp, stride_col, 0, c1, t, n);
+    return log_row_finish<F, St, TPR, UNROLL, VECTOR>(s, rp, stride_col, c1, t, n, lds_state,
+                                                      lds_lane);
   } else {
     const State e = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, 0, c1, t, n,
                                                                  lds_state);
-    result = finalize_state<F>(e, n);
+    return finalize_state<F>(e, n);
   }
+}
+
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, int WG>
+__device__ __forceinline__ void fold_serial(const typename St::T* __restrict__ x,
+                                            typename St::T* __restrict__ out, i64 rows,
+                                            i64 ncols, i64 stride_row, i64 stride_col) {
+  static_assert(WG % 64 == 0 && (TPR <= 64 || WG % TPR == 0), "bad row mapping");
+  constexpr int RPW = WG / TPR;  // rows per workgroup
+  __shared__ State lds_state[WG / 64];
+  __shared__ LogLane lds_lane[WG / 64];
+  const int t = threadIdx.x % TPR;
+  const i64 row = (i64)blockIdx.x * RPW + threadIdx.x / TPR;
+  const bool live = row < rows;
+  const typename St::T* rp = x + (live ? row : 0) * stride_row;
+  const i64 c1 = live ? ncols : 0;
+  const float n = (float)ncols;
+  const float result =
+      row_result<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c1, t, n, lds_state, lds_lane);
   if (live && t == 0) St::store(out + row, result);
+}
+
+// Readout of an exponential fold (log-softmax for logsumexp): out[row, c] = phi(x[row, c]) -
+// r, r the row's fp32 result, computed in fp32 and rounded once to the storage type; with
+// NAN_POSINF a row whose r is +inf (a +inf element) reads out NaN everywhere, as the lowered
+// `where(lse == inf, nan, x - lse)` does.  `out` is contiguous [rows, ncols].  A row that
+// fits in one tile stays in registers between the fold and the readout (one HBM read);
+// wider rows are read twice.
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, int WG, bool NAN_POSINF>
+__device__ __forceinline__ void fold_readout(const typename St::T* __restrict__ x,
+                                             typename St::T* __restrict__ out, i64 rows,
+                                             i64 ncols, i64 stride_row, i64 stride_col) {
+  static_assert(F::kLog, "the readout is defined for exponential folds");
+  static_assert(WG % 64 == 0 && (TPR <= 64 || WG % TPR == 0), "bad row mapping");
+  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+  constexpr int RPW = WG / TPR;
+  __shared__ State lds_state[WG / 64];
+  __shared__ LogLane lds_lane[WG / 64];
+  const int t = threadIdx.x % TPR;
+  const i64 row = (i64)blockIdx.x * RPW + threadIdx.x / TPR;
+  const bool live = row < rows;
+  const typename St::T* rp = x + (live ? row : 0) * stride_row;
+  typename St::T* op = out + (live ? row : 0) * ncols;
+  const i64 c1 = live ? ncols : 0;
+  const float n = (float)ncols;
+  if (ncols <= TL::TILE) {
+    RawTile<St, UNROLL, VECTOR> keep;
+    load_raw<St, TPR, UNROLL, VECTOR>(keep, rp, stride_col, 0, c1, t);
+    LogLane s;
+    s.m = -kInf;
+    s.acc = 0.0f;
+    s.flag = 0;
+    log_fold_tile<F, St, TPR, UNROLL, VECTOR, true>(s, keep, n);
+    const float r = log_row_finish<F, St, TPR, UNROLL, VECTOR>(s, rp, stride_col, c1, t, n,
+                                                               lds_state, lds_lane);
+    const bool nan_row = NAN_POSINF && r == kInf;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (!keep.ok[u]) continue;
+      const i64 e = (i64)(u * TPR + t) * TL::VEC;
+      if constexpr (VECTOR) {
+        float v[TL::VEC];
+        St::unpack(keep.w[u], v);
+#pragma unroll
+        for (int j = 0; j < TL::VEC; ++j)
+          v[j] = nan_row ? __builtin_nanf("") : (F::phi(v[j], n) - r);
+        store16(op + e, St::pack(v));
+      } else {
+        St::store(op + e, nan_row ? __builtin_nanf("") : (F::phi(keep.s[u], n) - r));
+      }
+    }
+    return;
+  }
+  const float r = row_result<F, St, TPR, UNROLL, VECTOR, true>(rp, stride_col, c1, t, n,
+                                                              lds_state, lds_lane);
+  const bool nan_row = NAN_POSINF && r == kInf;
+  for (i64 tile = 0; tile < c1; tile += TL::TILE) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const i64 e = tile + (i64)(u * TPR + t) * TL::VEC;
+      if (e >= c1) continue;
+      if constexpr (VECTOR) {
+        float v[TL::VEC];
+        St::unpack(load16(rp + e), v);
+#pragma unroll
+        for (int j = 0; j < TL::VEC; ++j)
+          v[j] = nan_row ? __builtin_nanf("") : (F::phi(v[j], n) - r);
+        store16(op + e, St::pack(v));
+      } else {
+        const float v = St::load(rp + e * stride_col);
+        St::store(op + e, nan_row ? __builtin_nanf("") : (F::phi(v, n) - r));
+      }
+    }
+  }
 }
 
 // Split plan, partial kernel (template.py:137-148): virtual row vr = row*nparts + part covers

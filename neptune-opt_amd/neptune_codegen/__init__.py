@@ -27,11 +27,13 @@ from neptune_codegen.skeleton import (NEGATIVE_CONTROLS, SKELETONS, STATE_REDUCT
 from neptune_codegen.sym_to_hip import TranslationError, to_hip
 from neptune_codegen.symbols import *  # noqa: F401,F403
 from neptune_codegen.template import (MAX_SPLIT_PARTS, compile_skeleton, compile_state_reduction,
-                                      generated_path, launch_reduction, launch_rms_norm, run,
-                                      run_l2_normalize, run_rms_norm, split_launch_shape,
+                                      compile_readout, generated_path, launch_reduction,
+                                      launch_rms_norm, run, run_l2_normalize, run_log_softmax,
+                                      run_readout, run_rms_norm, split_launch_shape,
                                       validate_l2_inputs, validate_plan, validate_rms_inputs)
-from neptune_codegen.torch_op import (as_hip_op, as_segment_op, as_state_op, as_triton_op,
-                                      compile_segment_reduction, op_handle, run_segment_pool,
+from neptune_codegen.torch_op import (as_hip_op, as_readout_op, as_segment_op, as_state_op,
+                                      as_triton_op, compile_segment_reduction, op_handle,
+                                      readout_op_handle, run_segment_pool,
                                       segment_op_handle, state_op_handle, triton_op_name,
                                       validate_segment_inputs)
 
@@ -60,5 +62,6 @@ __all__ = [
     "state_op_handle", "as_segment_op", "segment_op_handle", "run_segment_pool",
     "compile_segment_reduction", "validate_segment_inputs",
     "run_attention", "attention_fold", "as_attention_op",
+    "compile_readout", "run_readout", "run_log_softmax", "as_readout_op", "readout_op_handle",
     "best_config", "machine_key", "op_key", "parameter_tag", "prebuilt_programs",
 ]

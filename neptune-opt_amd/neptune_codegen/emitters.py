@@ -281,6 +281,36 @@ def emit_kernel_source(sk: Skeleton, values: dict | None = None, *, plan: str = 
     return "\n".join(parts)
 
 
+def readout_kernel_name(sk: Skeleton, var: FoldVariant, nan_posinf_rows: bool) -> str:
+    return f"{sk.name}_readout{'_nanrows' if nan_posinf_rows else ''}_{var.tag()}"
+
+
+def emit_readout_source(sk: Skeleton, values: dict | None = None, *, variants: tuple,
+                        nan_posinf_rows: bool = True) -> str:
+    """A hiprtc unit of the readout phi(x) - r of an exponential fold (log-softmax for
+    logsumexp), one kernel per launch shape; see nep_fold.h fold_readout."""
+    check_supported(sk)
+    if not sk.is_log or sk.two_pass:
+        raise NotImplementedError(f"skeleton {sk.name!r}: the readout needs an exponential fold")
+    header = (f"// AUTO-GENERATED by neptune_codegen (HIP emitter) -- do not edit.\n"
+              f"// skeleton={sk.name!r}, readout phi(x) - r, nan_posinf_rows={nan_posinf_rows}\n")
+    parts = [header, kernel_header("nep_device.h", "nep_fold.h"), emit_fold_policy(sk, values)]
+    flag = "true" if nan_posinf_rows else "false"
+    seen = set()
+    for var in variants:
+        _, st = dtype_tag(var.dtype)
+        vec = "true" if var.vector else "false"
+        name = readout_kernel_name(sk, var, nan_posinf_rows)
+        if name in seen:
+            continue
+        seen.add(name)
+        parts.append(
+            f'extern "C" __global__ void __launch_bounds__({var.wg}) {name}({_FOLD_ARGS_SERIAL}) {{\n'
+            f"  nep::fold_readout<Fold, {st}, {var.tpr}, {var.unroll}, {vec}, {var.wg}, {flag}>("
+            f"(const {st}::T*)x, ({st}::T*)out, rows, ncols, stride_row, stride_col);\n}}\n")
+    return "\n".join(parts)
+
+
 def fold_kernel_name(sk: Skeleton, plan: str, stage: str, var: FoldVariant) -> str:
     kind = "two_pass" if sk.two_pass else plan
     return _fold_kernel(sk, kind, stage, var)[0]

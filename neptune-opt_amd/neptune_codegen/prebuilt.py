@@ -29,6 +29,12 @@ def _fold_programs():
         params = {**param_defaults(name), **({"eps": 1e-6} if name == "rmsnorm_max" else {})}
         prog = compile_skeleton(name, params)
         out.append(prog.program(_fold_variant(x2, 4096, block, warps, resident=prog.sk.two_pass)))
+    from neptune_codegen.template import compile_readout
+
+    xw = torch.empty((16384, 32000), device="meta", dtype=torch.bfloat16)
+    block, warps = best_config(16384, 32000, torch.bfloat16, None, device_name="gfx950")
+    out.append(compile_readout("logsumexp").program(
+        _fold_variant(xw, 32000, block, warps, resident=True)))
     x2 = torch.empty((64, 262144), device="meta", dtype=torch.bfloat16)
     partial, _merge = compile_skeleton("logsumexp", lse, plan="split")
     out.append(partial.program(_fold_variant(x2, 262144, 1024, 4, split_block=1024)))

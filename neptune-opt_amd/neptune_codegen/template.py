@@ -17,9 +17,10 @@ from neptune_codegen import hip
 from neptune_codegen.autotune import (MAX_TPR, MAX_UNROLL, UNROLL, best_config, lanes_per_row,
                                       parameter_identity, parameter_tag, vec_of)
 from neptune_codegen.emitters import (BASE_OPTIONS, NO_CONTRACT, FoldVariant, RowVariant,
-                                      check_supported, emit_kernel_source, emit_rms_state_source,
-                                      fold_kernel_name, rms_kernel_names)
-from neptune_codegen.skeleton import SKELETONS, all_registered
+                                      check_supported, emit_kernel_source, emit_readout_source,
+                                      emit_rms_state_source, fold_kernel_name,
+                                      readout_kernel_name, rms_kernel_names)
+from neptune_codegen.skeleton import SKELETONS, all_registered, param_defaults
 
 MAX_SPLIT_PARTS = 4096
 _CACHE: dict = {}
@@ -102,6 +103,92 @@ class FoldProgram:
             args = (hip.PTR, hip.PTR) + (hip.I64,) * 4
             block = var.wg
         return self.program(var).kernel(name, args, block, device)
+
+
+class ReadoutProgram:
+    """The readout kernels phi(x) - r of one exponential fold (log-softmax for logsumexp)."""
+
+    def __init__(self, name: str, values: dict, nan_posinf_rows: bool):
+        self.name, self.values, self.nan_posinf_rows = name, dict(values), nan_posinf_rows
+        self.sk = SKELETONS[name]
+        self._programs: dict = {}
+
+    def source(self, var: FoldVariant) -> str:
+        return emit_readout_source(self.sk, self.values, variants=(var,),
+                                   nan_posinf_rows=self.nan_posinf_rows)
+
+    def program(self, var: FoldVariant) -> hip.Program:
+        prog = self._programs.get(var)
+        if prog is None:
+            tag = "_nanrows" if self.nan_posinf_rows else ""
+            prog = hip.Program(self.source(var), f"{self.name}_readout{tag}_{var.tag()}.hip",
+                               BASE_OPTIONS)
+            self._programs[var] = prog
+        return prog
+
+    def kernel(self, var: FoldVariant, device: int) -> hip.Kernel:
+        name = readout_kernel_name(self.sk, var, self.nan_posinf_rows)
+        return self.program(var).kernel(name, (hip.PTR, hip.PTR) + (hip.I64,) * 4, var.wg, device)
+
+
+def compile_readout(name: str, values: dict | None = None, *, nan_posinf_rows: bool = True):
+    """The readout program of an exponential fold; refusals surface here, before any launch."""
+    values = {**param_defaults(name), **(values or {})} if name in SKELETONS else values
+    key = ("readout", name, parameter_identity(values), bool(nan_posinf_rows))
+    with _cache_lock:
+        if key in _CACHE:
+            return _CACHE[key]
+    if name not in SKELETONS:
+        raise KeyError(f"unknown skeleton {name!r}; have {all_registered()}")
+    emit_readout_source(SKELETONS[name], values, variants=(), nan_posinf_rows=nan_posinf_rows)
+    program = ReadoutProgram(name, values or {}, bool(nan_posinf_rows))
+    with _cache_lock:
+        _CACHE[key] = program
+    return program
+
+
+def launch_readout(program: ReadoutProgram, x2, out, rows, ncols, block, num_warps) -> None:
+    """Launch a readout on the current stream: out [rows, ncols] contiguous."""
+    import torch
+
+    device = x2.device.index if x2.device.index is not None else torch.cuda.current_device()
+    var = _fold_variant(x2, ncols, block, num_warps, resident=True)
+    rpw = max(1, var.wg // var.tpr)
+    program.kernel(var, device).launch(
+        (_grid_1d(rows, rpw),),
+        (x2.data_ptr(), out.data_ptr(), rows, ncols, x2.stride(0), x2.stride(1)),
+        hip.current_stream(x2.device))
+
+
+def run_readout(name: str, x, *, nan_posinf_rows: bool = True, block: int | None = None,
+                num_warps: int | None = None, **params):
+    """phi(x) - r over the last dimension, r the row's exponential fold (fp32), rounded once to
+    x.dtype: for logsumexp, log_softmax(x, -1).  With nan_posinf_rows a row containing +inf
+    reads out NaN, as the reference's log_softmax lowering does (lowering.py:92-98).  Fresh
+    contiguous output of x's shape and dtype; Fake/meta tensors return metadata only."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensor
+
+    metadata = isinstance(x, FakeTensor) or x.device.type == "meta"
+    _validate_row_last(x, metadata=metadata)
+    program = compile_readout(name, params, nan_posinf_rows=nan_posinf_rows)
+    out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    if metadata:
+        return out
+    x2, rows, ncols = _row_last_layout(x)
+    if isinstance(rows, int) and rows == 0:
+        return out
+    if block is None or num_warps is None:
+        cfg = best_config(rows, ncols, x.dtype, x.device)
+        block = cfg[0] if block is None else block
+        num_warps = cfg[1] if num_warps is None else num_warps
+    launch_readout(program, x2, out, rows, ncols, block, num_warps)
+    return out
+
+
+def run_log_softmax(x, *, nan_posinf_rows: bool = True):
+    """log_softmax over the last dimension through the logsumexp fold's readout."""
+    return run_readout("logsumexp", x, nan_posinf_rows=nan_posinf_rows)
 
 
 def compile_skeleton(name: str, values: dict | None = None, force: bool = False, *,

@@ -107,6 +107,57 @@ def triton_op_name(name: str, lib: str = "neptune") -> str:
     return f"{lib}.{name}"
 
 
+def as_readout_op(name: str, params: dict | None = None, nan_posinf_rows: bool = True,
+                  lib: str = "neptune", block: int | None = None, num_warps: int | None = None):
+    """Custom op `(Tensor x) -> Tensor`: the readout phi(x) - r of the exponential fold `name`
+    (log_softmax for logsumexp), output of x's shape and dtype.  The name is the fold's op key
+    plus `_readout` (`_readout_nanrows` when +inf rows read out NaN)."""
+    from neptune_codegen.template import compile_readout, launch_readout
+
+    params = {**param_defaults(name), **(params or {})}
+    key = autotune.op_key(lib, name, params, False, block, num_warps)
+    key += "_readout_nanrows" if nan_posinf_rows else "_readout"
+    with _lock:
+        if key in _TRITON_OPS:
+            return _TRITON_OPS[key]
+    import torch
+
+    program = compile_readout(name, params, nan_posinf_rows=nan_posinf_rows)
+    impl_name = key.split("::", 1)[1]
+
+    def _impl(x):
+        _validate_row_last(x)
+        x2, rows, ncols = _row_last_layout(x)
+        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+        if isinstance(rows, int) and rows == 0:
+            return out
+        cfg = (block, num_warps)
+        if block is None or num_warps is None:
+            chosen = autotune.best_config(rows, ncols, x.dtype, x.device)
+            cfg = (chosen[0] if block is None else block, chosen[1] if num_warps is None else num_warps)
+        launch_readout(program, x2, out, rows, ncols, cfg[0], cfg[1])
+        return out
+
+    def _fake(x):
+        _validate_row_last(x, metadata=True)
+        return torch.empty(x.shape, device=x.device, dtype=x.dtype)
+
+    op = _register(key, "(Tensor x) -> Tensor", _impl, _fake)
+    dispatch.install(key, 1, _impl)
+    op.__name__ = f"{lib}_{impl_name}"
+    with _lock:
+        _TRITON_OPS[key] = op
+    return op
+
+
+def readout_op_handle(name: str, params: dict | None = None, nan_posinf_rows: bool = True,
+                      lib: str = "neptune", block: int | None = None,
+                      num_warps: int | None = None):
+    """The OpOverload of a fold's readout op, for building graph nodes."""
+    return _overload(lib, as_readout_op(name, params=params, nan_posinf_rows=nan_posinf_rows,
+                                        lib=lib, block=block, num_warps=num_warps))
+
+
 # ---------------------------------------------------------------- structured row ops
 _STATE_OPS: dict[tuple, object] = {}
 

@@ -226,7 +226,8 @@ def rewrite_match(gm, match, *, lib="neptune", plan="serial"):
         if not node.users and not node.is_impure():
             graph.erase_node(node)
     if getattr(match, "kind", "scalar") != "structured":
-        call = _absorb_casts(gm, call, match, keepdim, lib, plan)
+        fused = _fuse_readout(gm, call, match, keepdim, lib, plan)
+        call = fused if fused is not call else _absorb_casts(gm, call, match, keepdim, lib, plan)
     graph.lint()
     gm.recompile()
     return call, None
@@ -262,6 +263,77 @@ def _dtype_cast(node, source=None):
     if source is not None and node.args[0] is not source:
         return None
     return dtype
+
+
+def _only_users(node, skip_checks: bool = True):
+    return [u for u in node.users if not (skip_checks and _is_metadata_assert(u))]
+
+
+def _fuse_readout(gm, call, match, keepdim, lib, plan):
+    """lse = logsumexp fold (keepdim) read only as x - lse, optionally through
+    where(lse == inf, nan, x - lse) -- the log_softmax readout of the compound lowering
+    (lowering.py's readout steps) -- becomes one readout op writing the whole row
+    (neptune_codegen.run_readout); a 16-bit input reached through its fp32 widening, with the
+    result narrowed back, is read directly."""
+    import math
+
+    import torch
+
+    if match.skeleton != "logsumexp" or not keepdim or plan != "serial":
+        return call
+    params = {**CG.param_defaults(match.skeleton), **match.params}
+    if params.get("tiny", 0.0) != 0.0:
+        return call
+    aten = torch.ops.aten
+    x = call.args[0]
+    users = _only_users(call)
+    sub = next((u for u in users if u.target is aten.sub.Tensor), None)
+    if sub is None or sub.args != (x, call) or sub.kwargs:
+        return call
+    final, nan_rows, dropped = sub, False, [sub]
+    if len(users) == 2:
+        eq = next(u for u in users if u is not sub)
+        if eq.target is not aten.eq.Scalar or eq.args != (call, math.inf) or eq.kwargs:
+            return call
+        where = list(sub.users)
+        if (len(where) != 1 or list(eq.users) != where
+                or where[0].target is not aten.where.ScalarSelf or where[0].kwargs):
+            return call
+        cond, fill, other = where[0].args
+        if cond is not eq or other is not sub or not (isinstance(fill, float) and math.isnan(fill)):
+            return call
+        final, nan_rows, dropped = where[0], True, [where[0], sub, eq]
+    elif len(users) != 1:
+        return call
+    source = x
+    if _dtype_cast(x) is torch.float32:
+        value = _tensor_value(x.args[0])
+        narrow = list(final.users)
+        if (value is not None and value.dtype in (torch.bfloat16, torch.float16)
+                and len(narrow) == 1 and _dtype_cast(narrow[0], final) is value.dtype):
+            source = x.args[0]
+            dropped.insert(0, narrow[0])
+            final = narrow[0]
+    graph = gm.graph
+    op = CG.readout_op_handle("logsumexp", params=params, nan_posinf_rows=nan_rows, lib=lib)
+    with graph.inserting_before(final):
+        fused = graph.call_function(op, args=(source,))
+    fused.meta = copy.copy(final.meta)
+    renamed = copy.deepcopy(gm.meta.get("neptune_replaced_roots", {}))
+    for old, new in list(renamed.items()):
+        if new == call.name:
+            renamed[old] = fused.name
+    renamed[final.name] = fused.name
+    gm.meta["neptune_replaced_roots"] = renamed
+    final.replace_all_uses_with(fused)
+    for node in dropped:
+        graph.erase_node(node)
+    for check in [u for u in call.users if _is_metadata_assert(u)]:
+        graph.erase_node(check)
+    graph.erase_node(call)
+    if source is not x and not x.users:
+        graph.erase_node(x)
+    return fused
 
 
 def _absorb_casts(gm, call, match, keepdim, lib, plan):

@@ -203,3 +203,76 @@ def test_split_back_to_back_calls_and_graph_replays():
         _say(f"split graph replay {replay}")
         _check("logsumexp", x, out)
         _check("logsumexp", x, CG.run("logsumexp", xd, plan="split"))   # eager in between
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_log_softmax_readout(dtype):
+    """run_log_softmax = x - logsumexp(x) per row, fp32, rounded once to x.dtype."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(21)
+    for rows, width in ((5, 1), (33, 77), (16, 1000), (3, 5000), (4, 40000)):
+        x = (4 * torch.randn(rows, width, generator=g)).to(dtype)
+        _say(f"log_softmax readout {dtype} [{rows},{width}]")
+        got = CG.run_log_softmax(x.to(dev)).cpu()
+        z = x.float()
+        want = z - torch.logsumexp(z, -1, keepdim=True)
+        assert got.dtype == dtype and got.shape == x.shape
+        if dtype == torch.float32:
+            scale = want.abs().amax().item() + 1.0
+            torch.testing.assert_close(got, want, rtol=1e-5, atol=2e-6 * scale)
+        else:
+            # one rounding of a value within a few fp32 ulps of the exact one: <= 1 storage ulp
+            ref = want.to(dtype).float()
+            ulp = torch.finfo(dtype).eps * want.abs().clamp_min(torch.finfo(dtype).tiny)
+            assert ((got.float() - ref).abs() <= ulp * 1.01 + 1e-30).all()
+    xs = torch.randn(64, 96, generator=g)[:, ::3].to(dtype)          # strided columns
+    _say(f"log_softmax readout strided {dtype}")
+    got = CG.run_log_softmax(xs.to(dev)).cpu().float()
+    want = torch.log_softmax(xs.float(), -1)
+    torch.testing.assert_close(got, want.to(dtype).float(), **dict(zip(("rtol", "atol"), TOL[dtype])))
+
+
+def test_log_softmax_readout_nonfinite_rows():
+    """+inf rows read out NaN (the lowering's where(lse == inf, nan, x - lse)); NaN rows NaN;
+    all -inf rows NaN (-inf - -inf); -inf elements of finite rows -inf."""
+    dev = _dev()
+    x = torch.randn(6, 300, generator=torch.Generator().manual_seed(22))
+    x[0, 7] = float("inf")
+    x[1, 9] = float("nan")
+    x[2] = float("-inf")
+    x[3, :150] = float("-inf")
+    x[4, 0] = float("inf")
+    x[4, 1] = float("-inf")
+    got = CG.run_log_softmax(x.to(dev)).cpu()
+    lse = torch.logsumexp(x, -1, keepdim=True)
+    want = torch.where(lse == float("inf"), float("nan"), x - lse)
+    assert torch.equal(torch.isnan(got), torch.isnan(want))
+    ok = ~torch.isnan(want)
+    torch.testing.assert_close(got[ok], want[ok], rtol=1e-5, atol=1e-5)
+    plain = CG.run_log_softmax(x.to(dev), nan_posinf_rows=False).cpu()
+    want_plain = x - lse
+    assert torch.equal(torch.isnan(plain), torch.isnan(want_plain))
+    ok = ~torch.isnan(want_plain)
+    torch.testing.assert_close(plain[ok], want_plain[ok], rtol=1e-5, atol=1e-5)
+
+
+def test_log_softmax_graph_through_apply():
+    """neptune_opt.apply with the experimental log_softmax lowering runs one readout op on the
+    device and verifies against torch (16-bit outputs within 2 ULP)."""
+    import neptune_opt
+
+    dev = _dev()
+
+    class LS(torch.nn.Module):
+        def forward(self, x):
+            return torch.log_softmax(x, dim=-1)
+
+    x = (4 * torch.randn(512, 4096, generator=torch.Generator().manual_seed(23))).bfloat16().to(dev)
+    model = LS().eval()
+    ep = torch.export.export(model, (x,))
+    report = neptune_opt.apply(ep, verify_with=(model, (x,)), experimental_log_softmax=True,
+                               max_ulps=2)
+    _say(report.summary())
+    assert report.fusions and report.verified is True
+    targets = [str(n.target) for n in ep.graph_module.graph.nodes if n.op == "call_function"]
+    assert targets == ["neptune.logsumexp_tiny0_readout_nanrows.default"], targets

@@ -257,3 +257,109 @@ def test_metadata_asserts_do_not_keep_a_fused_region_alive():
     assert leftover == [], leftover
     asserts = [n for n in _calls(ep) if n.target is torch.ops.aten._assert_tensor_metadata.default]
     assert all(n.args[0].op == "placeholder" for n in asserts)
+
+
+@torch.library.custom_op("neptune_cpu_standin::log_softmax_nanrows", mutates_args=())
+def _ls_nan(x: torch.Tensor) -> torch.Tensor:
+    z = x.float()
+    lse = torch.logsumexp(z, -1, keepdim=True)
+    return torch.where(lse == float("inf"), float("nan"), z - lse).to(x.dtype)
+
+
+@_ls_nan.register_fake
+def _(x):
+    return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("neptune_cpu_standin::log_softmax_plain", mutates_args=())
+def _ls_plain(x: torch.Tensor) -> torch.Tensor:
+    z = x.float()
+    return (z - torch.logsumexp(z, -1, keepdim=True)).to(x.dtype)
+
+
+@_ls_plain.register_fake
+def _(x):
+    return x.new_empty(x.shape)
+
+
+class LogSoftmax(torch.nn.Module):
+    def forward(self, x):
+        return torch.log_softmax(x, dim=-1)
+
+
+class MinusLSE(torch.nn.Module):
+    def forward(self, x):
+        return x - torch.logsumexp(x, dim=-1, keepdim=True)
+
+
+def _readout_standin():
+    asked = []
+
+    def handle(name, params=None, nan_posinf_rows=True, lib="neptune", **kw):
+        asked.append((name, nan_posinf_rows))
+        return (_ls_nan if nan_posinf_rows else _ls_plain)._opoverload
+
+    return asked, patch("neptune_codegen.readout_op_handle", handle)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_log_softmax_lowering_fuses_into_one_readout(dtype):
+    """log_softmax lowers to the LSE region plus x - lse and a NaN select for +inf rows; the
+    rewrite replaces all of it (and a 16-bit input's cast pair) with one readout op."""
+    x = (3 * torch.randn(16, 64, generator=torch.Generator().manual_seed(8))).to(dtype)
+    x[3, 5] = float("inf")
+    model = LogSoftmax().eval()
+    ep = torch.export.export(model, (x,))
+    asked, readout = _readout_standin()
+    a, b = _standin(_lse._opoverload)
+    with a, b, readout:
+        report = neptune_opt.apply(ep, verify_with=(model, (x,)), experimental_log_softmax=True,
+                                   max_ulps=2)
+    assert report.fusions and report.verified is True, report.summary()
+    assert asked == [("logsumexp", True)]
+    calls = _calls(ep)
+    assert [n.target for n in calls] == [_ls_nan._opoverload]
+    assert calls[0].args[0].op == "placeholder"
+    out = ep.module()(x)
+    assert out.dtype == dtype and torch.isnan(out[3]).all()
+
+
+def test_x_minus_lse_fuses_without_the_nan_select():
+    x = (3 * torch.randn(16, 64, generator=torch.Generator().manual_seed(9)))
+    model = MinusLSE().eval()
+    ep = torch.export.export(model, (x,))
+    asked, readout = _readout_standin()
+    a, b = _standin(_lse._opoverload)
+    with a, b, readout:
+        report = neptune_opt.apply(ep, verify_with=(model, (x,)))
+    assert report.fusions and report.verified is True, report.summary()
+    assert asked == [("logsumexp", False)]
+    assert [n.target for n in _calls(ep)] == [_ls_plain._opoverload]
+
+
+@torch.library.custom_op("neptune_cpu_standin::lse_keepdim", mutates_args=())
+def _lse_keep(x: torch.Tensor) -> torch.Tensor:
+    return torch.logsumexp(x, -1, keepdim=True)
+
+
+@_lse_keep.register_fake
+def _(x):
+    return x.new_empty(x.shape[:-1] + (1,))
+
+
+def test_lse_with_other_users_is_not_turned_into_a_readout():
+    class Both(torch.nn.Module):
+        def forward(self, x):
+            lse = torch.logsumexp(x, dim=-1, keepdim=True)
+            return x - lse, lse * 2
+
+    x = torch.randn(16, 64, generator=torch.Generator().manual_seed(10))
+    model = Both().eval()
+    ep = torch.export.export(model, (x,))
+    asked, readout = _readout_standin()
+    a, b = _standin(_lse_keep._opoverload)
+    with a, b, readout:
+        report = neptune_opt.apply(ep, verify_with=(model, (x,)))
+    assert report.fusions, report.summary()
+    assert asked == []
+    assert _lse_keep._opoverload in [n.target for n in _calls(ep)]
