@@ -13,6 +13,8 @@
  *   nep_compile_code_object  the device-independent half of nep_compile (hiprtc only, no GPU
  *                            needed); used to pre-build the on-disk code-object cache and to
  *                            check that every emitted kernel compiles for gfx950.
+ *   nep_module_load          loads a prebuilt code object (a launch-plan bundle's kernels)
+ *                            without hiprtc; see its declaration.
  *   nep_get_kernel           replaces getattr(module, name) after the import
  *                            (template.py:219-220, torch_op.py:332).
  *   nep_launch               replaces kernel[grid](args..., BLOCK=, num_warps=)
@@ -75,7 +77,15 @@ int nep_compile_code_object(const char* source, const char* name, const char* op
 /* Release a buffer returned by nep_compile_code_object. */
 void nep_free(void* buffer);
 
-/* Look up an extern "C" kernel in a module returned by nep_compile. */
+/*
+ * Load a gfx950 code object (the bytes nep_compile_code_object produced) as a module on the
+ * current device.  This is how a launch-plan bundle brings its kernels into a process that
+ * never compiles: it replaces the reference's load of the Triton binary an AOTI package
+ * embeds (neptune_opt/ab.py:95-255 packages it; docs/design.md:283-287).  Not cached.
+ */
+int nep_module_load(const void* image, size_t size, uint64_t* module_out);
+
+/* Look up an extern "C" kernel in a module returned by nep_compile or nep_module_load. */
 int nep_get_kernel(uint64_t module, const char* kernel_name, uint64_t* kernel_out);
 
 /*

@@ -2,7 +2,8 @@
 
 1. hipcc builds the C-ABI runtime libneptune_hip.so (host code: hiprtc + module launch) in
    place, next to the Python package, so that it travels with the source tree; g++ builds
-   the operators' C++ dispatcher kernels (_neptune_dispatch.so) beside it.
+   the operators' C++ dispatcher kernels (_neptune_dispatch.so) and the Python-free
+   launch-plan bundle loader (libneptune_ops.so) beside it.
 2. Every generated kernel unit the benchmark configurations and tests use is compiled with
    hiprtc for gfx950 into the on-disk code-object cache (neptune_codegen/_codeobj).  That both
    proves each emitted unit compiles and spares the GPU host the compile.
@@ -64,6 +65,31 @@ def build_dispatch(verbose: bool = True) -> pathlib.Path:
     return DISPATCH
 
 
+OPS = ROOT / "neptune_codegen" / "_lib" / "libneptune_ops.so"
+OPS_SRC = ROOT / "csrc" / "nep_ops.cpp"
+
+
+def build_ops(verbose: bool = True) -> pathlib.Path:
+    """g++: the Python-free bundle loader (libtorch + libneptune_hip only)."""
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = cpp_extension.library_paths()[0]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = OPS.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-fPIC", "-shared", "-std=c++17",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *(f"-I{p}" for p in cpp_extension.include_paths()), "-I/opt/rocm/include",
+           f"-I{REPO / 'include'}", str(OPS_SRC), "-o", str(tmp),
+           f"-L{torch_lib}", f"-L{LIB.parent}", "-lneptune_hip", "-lc10", "-lc10_hip",
+           "-ltorch", "-ltorch_cpu", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
+    if verbose:
+        print("[build]", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, OPS)
+    return OPS
+
+
 def precompile(verbose: bool = True) -> int:
     """hiprtc-compile the kernel units of the benchmark and test shapes into the cache."""
     sys.path.insert(0, str(ROOT))
@@ -81,6 +107,7 @@ def precompile(verbose: bool = True) -> int:
 def main() -> None:
     build_library()
     build_dispatch()
+    build_ops()
     precompile()
 
 

@@ -20,60 +20,25 @@
 // no plan and keep going through Python.
 #include <ATen/core/dispatch/Dispatcher.h>
 #include <ATen/core/grad_mode.h>
-#include <ATen/ops/empty_strided.h>
-#include <c10/hip/HIPStream.h>
 #include <torch/csrc/utils/pybind.h>
 #include <torch/library.h>
 
-#include <cstring>
 #include <memory>
 #include <mutex>
 #include <string>
 #include <unordered_map>
 #include <vector>
 
-#include "../../include/neptune_hip.h"
+#include "nep_plan.h"
 
 namespace py = pybind11;
 
 namespace {
 
-constexpr size_t kMaxImage = 1024;
-
-struct Launch {
-  uint64_t kernel = 0;
-  uint32_t grid[3] = {1, 1, 1};
-  uint32_t block = 0;
-  uint32_t lds = 0;
-  std::vector<uint8_t> image;
-  // (byte offset in the image, source): source >= 0 is input `source`, source < 0 is
-  // buffer (-1 - source); outputs are the first buffers.
-  std::vector<std::pair<uint32_t, int32_t>> patches;
-};
-
-struct Buffer {
-  std::vector<int64_t> sizes, strides;
-  c10::ScalarType dtype;
-};
-
-struct Plan {
-  bool replayable = false;
-  std::vector<Buffer> buffers;
-  std::vector<Launch> launches;
-};
-
-using Key = std::vector<int64_t>;
-
-struct KeyHash {
-  size_t operator()(const Key& key) const noexcept {
-    uint64_t h = 1469598103934665603ull;
-    for (int64_t v : key) {
-      h ^= static_cast<uint64_t>(v);
-      h *= 1099511628211ull;
-    }
-    return static_cast<size_t>(h);
-  }
-};
+using nep_plan::Key;
+using nep_plan::KeyHash;
+using nep_plan::Launch;
+using nep_plan::Plan;
 
 // Python callables are held as leaked references: the dispatcher may destroy kernels after
 // the interpreter has finalised, when a Py_DECREF would be unsafe.
@@ -140,27 +105,7 @@ class PlanKernel final : public c10::OperatorKernel {
 
  private:
   bool make_key(c10::ArrayRef<c10::IValue> args, Key& key) const {
-    std::vector<uintptr_t> ptrs;
-    ptrs.reserve(args.size());
-    for (const c10::IValue& arg : args) {
-      if (!arg.isTensor()) return false;
-      const at::Tensor& t = arg.toTensor();
-      if (!t.defined() || t.device().type() != device_type_ || t.layout() != c10::kStrided ||
-          t.is_neg() || t.is_conj())
-        return false;
-      const auto uptr = reinterpret_cast<uintptr_t>(t.data_ptr());
-      key.push_back(static_cast<int64_t>(t.scalar_type()));
-      key.push_back(t.get_device());
-      key.push_back(t.dim());
-      for (int64_t s : t.sizes()) key.push_back(s);
-      for (int64_t s : t.strides()) key.push_back(s);
-      key.push_back(static_cast<int64_t>(uptr % 16));
-      ptrs.push_back(uptr);
-    }
-    for (size_t i = 0; i < ptrs.size(); ++i)
-      for (size_t j = i + 1; j < ptrs.size(); ++j)
-        if (ptrs[i] == ptrs[j]) return false;  // aliased inputs: never replayed
-    return true;
+    return nep_plan::make_key(args, device_type_, key);
   }
 
   std::shared_ptr<Plan> parse_plan(const py::handle& spec) const {
@@ -182,50 +127,24 @@ class PlanKernel final : public c10::OperatorKernel {
       launch.block = lt[2].cast<uint32_t>();
       launch.lds = lt[3].cast<uint32_t>();
       std::string image = lt[4].cast<std::string>();
-      if (image.size() > kMaxImage) return std::make_shared<Plan>();
       launch.image.assign(image.begin(), image.end());
       for (py::handle p : lt[5].cast<py::tuple>()) {
         py::tuple pt = p.cast<py::tuple>();
-        const auto offset = pt[0].cast<uint32_t>();
-        const auto source = pt[1].cast<int32_t>();
-        if (offset + sizeof(void*) > launch.image.size()) return std::make_shared<Plan>();
-        if (source >= n_inputs_ || -1 - source >= static_cast<int32_t>(plan->buffers.size()))
-          return std::make_shared<Plan>();
-        launch.patches.emplace_back(offset, source);
+        launch.patches.emplace_back(pt[0].cast<uint32_t>(), pt[1].cast<int32_t>());
       }
       plan->launches.push_back(std::move(launch));
     }
     // launches need a HIP stream: only device plans may carry them
-    plan->replayable = !plan->buffers.empty() &&
+    plan->replayable = nep_plan::plan_consistent(*plan, n_inputs_) &&
                        (plan->launches.empty() || device_type_ == c10::DeviceType::CUDA);
     return plan;
   }
 
   at::Tensor replay(const Plan& plan, c10::ArrayRef<c10::IValue> args) {
-    const at::Tensor& first = args[0].toTensor();
-    const at::TensorOptions options = at::TensorOptions().device(first.device());
-    std::vector<at::Tensor> buffers;
-    buffers.reserve(plan.buffers.size());
-    for (const Buffer& b : plan.buffers)
-      buffers.push_back(at::empty_strided(b.sizes, b.strides, options.dtype(b.dtype)));
-    if (!plan.launches.empty()) {
-      hipStream_t stream = c10::hip::getCurrentHIPStream(first.get_device()).stream();
-      uint8_t image[kMaxImage];
-      for (const Launch& l : plan.launches) {
-        std::memcpy(image, l.image.data(), l.image.size());
-        for (const auto& [offset, source] : l.patches) {
-          void* ptr = source >= 0 ? args[source].toTensor().data_ptr()
-                                  : buffers[-1 - source].data_ptr();
-          std::memcpy(image + offset, &ptr, sizeof(ptr));
-        }
-        const int rc = nep_launch_packed(l.kernel, l.grid[0], l.grid[1], l.grid[2], l.block,
-                                         l.lds, stream, image, l.image.size());
-        TORCH_CHECK(rc == NEP_OK, "neptune launch failed: ", nep_last_error());
-      }
-    }
+    at::Tensor out = nep_plan::replay(plan, args);
     std::lock_guard<std::mutex> guard(mu_);
     stats_->replays += 1;
-    return buffers[0];
+    return out;
   }
 
   const int n_inputs_;
@@ -324,6 +243,16 @@ void clear() {
   for (auto& [name, entry] : registry()) entry.kernel->clear();
 }
 
+// The layout key the CUDA kernels compute for these inputs (None when the call has none).
+py::object key_of(const std::vector<at::Tensor>& tensors) {
+  std::vector<c10::IValue> args(tensors.begin(), tensors.end());
+  Key key;
+  if (!nep_plan::make_key(args, c10::DeviceType::CUDA, key)) return py::none();
+  return py::cast(key);
+}
+
+int64_t dtype_code(const at::Tensor& t) { return static_cast<int64_t>(t.scalar_type()); }
+
 bool installed(const std::string& qualname) {
   std::lock_guard<std::mutex> guard(g_mu);
   return registry().count(qualname) != 0;
@@ -338,4 +267,6 @@ PYBIND11_MODULE(_neptune_dispatch, m) {
   m.def("stats", &stats, py::arg("qualname"));
   m.def("clear", &clear);
   m.def("installed", &installed, py::arg("qualname"));
+  m.def("key_of", &key_of, py::arg("tensors"));
+  m.def("dtype_code", &dtype_code, py::arg("tensor"));
 }

@@ -193,6 +193,16 @@ int nep_compile(const char* source, const char* name, const char* options,
   return NEP_OK;
 }
 
+int nep_module_load(const void* image, size_t size, uint64_t* module_out) {
+  if (image == nullptr || size == 0 || module_out == nullptr)
+    return fail(NEP_ERR_INVALID, "nep_module_load: null or empty code object");
+  hipModule_t module = nullptr;
+  hipError_t err = hipModuleLoadData(&module, image);
+  if (err != hipSuccess) return hip_fail(err, "hipModuleLoadData");
+  *module_out = reinterpret_cast<uint64_t>(module);
+  return NEP_OK;
+}
+
 int nep_get_kernel(uint64_t module, const char* kernel_name, uint64_t* kernel_out) {
   if (module == 0 || kernel_name == nullptr || kernel_out == nullptr)
     return fail(NEP_ERR_INVALID, "nep_get_kernel: null argument");

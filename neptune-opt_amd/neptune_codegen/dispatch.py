@@ -25,12 +25,16 @@ Plans are per process; `clear()` drops them (after replacing the launch table, f
 from __future__ import annotations
 
 import importlib.util
+import struct
 import threading
 
 from neptune_codegen import hip
 
 _lock = threading.Lock()
 _module = None
+# qualname -> {"arguments": schema text after the name, "n_inputs": int,
+#              "plans": {key tuple: (plan, kernels)}}: what export_bundle writes
+_RECORDED: dict = {}
 MODULE_PATH = hip.LIB_PATH.parent / "_neptune_dispatch.so"
 
 
@@ -108,17 +112,96 @@ def install(qualname: str, n_inputs: int, body, *, backend: str = "CUDA") -> Non
     grad_keys = torch._C.DispatchKeySet(getattr(torch._C.DispatchKey, backend)).add(
         getattr(torch._C.DispatchKey, autograd_key))
 
+    schema = str(torch._C._get_schema(qualname, ""))
+    entry = {"arguments": schema[len(qualname):], "n_inputs": n_inputs, "plans": {}}
+
     def replayable_body(record, *inputs):
         if not record:
             return body(*inputs), None
         with hip.recording() as recorder:
             out = body(*inputs)
-        return out, plan_of(recorder, inputs, (out,))
+        plan = plan_of(recorder, inputs, (out,))
+        if plan is not None:
+            key = ext.key_of(list(inputs))
+            if key is not None:
+                with _lock:
+                    entry["plans"][tuple(key)] = (plan, [k for k, *_ in recorder.launches])
+        return out, plan
 
     def grad_body(*inputs):
         return original_autograd.call_boxed(grad_keys, *inputs)
 
     ext.install(qualname, n_inputs, replayable_body, grad_body, backend)
+    with _lock:
+        _RECORDED[qualname] = entry
+
+
+def recorded_layouts(qualname: str) -> int:
+    """How many input layouts of `qualname` have a recorded plan in this process."""
+    with _lock:
+        return len(_RECORDED.get(qualname, {}).get("plans", {}))
+
+
+def export_bundle(path, qualnames=None) -> int:
+    """Write the recorded launch plans of the installed operators (all, or `qualnames`) with
+    their kernels' code objects to `path`, for libneptune_ops (`torch.ops.neptune_bundle.load`
+    or `nep_ops_load_bundle`): a fused AOTI package then runs in a process without the Python
+    package.  Only layouts this process ran are included.  Returns the number of plans."""
+    ext = extension()
+    with _lock:
+        chosen = {q: e for q, e in _RECORDED.items()
+                  if (qualnames is None or q in qualnames) and e["plans"]}
+    if qualnames is not None:
+        missing = set(qualnames) - set(chosen)
+        if missing:
+            raise ValueError(f"no recorded launch plan for {sorted(missing)}; run the operator "
+                             "on the inputs to bundle first")
+    codes: list[bytes] = []
+    code_index: dict = {}
+    ops_blob = bytearray()
+    plans_written = 0
+
+    def put_str(buf, text):
+        data = text.encode()
+        buf += struct.pack("<I", len(data)) + data
+
+    ops_blob += struct.pack("<I", len(chosen))
+    for qualname, entry in chosen.items():
+        put_str(ops_blob, qualname)
+        put_str(ops_blob, entry["arguments"])
+        ops_blob += struct.pack("<II", entry["n_inputs"], len(entry["plans"]))
+        for key, ((buffers, launches), kernels) in entry["plans"].items():
+            ops_blob += struct.pack("<I", len(key)) + struct.pack(f"<{len(key)}q", *key)
+            ops_blob += struct.pack("<I", len(buffers))
+            for (tensor,) in buffers:
+                ops_blob += struct.pack("<iI", ext.dtype_code(tensor), tensor.dim())
+                ops_blob += struct.pack(f"<{tensor.dim()}q", *tensor.shape)
+                ops_blob += struct.pack(f"<{tensor.dim()}q", *tensor.stride())
+            ops_blob += struct.pack("<I", len(launches))
+            for (_handle, grid, block, lds, image, patches), kernel in zip(launches, kernels):
+                program = kernel.program
+                ident = (program.source, program.options)
+                if ident not in code_index:
+                    code_index[ident] = len(codes)
+                    codes.append(program.code_object())
+                ops_blob += struct.pack("<I", code_index[ident])
+                put_str(ops_blob, kernel.name)
+                ops_blob += struct.pack("<5I", *grid, block, lds)
+                ops_blob += struct.pack("<I", len(image)) + image
+                ops_blob += struct.pack("<I", len(patches))
+                for offset, source in patches:
+                    ops_blob += struct.pack("<Ii", offset, source)
+            plans_written += 1
+    blob = bytearray(b"NEPBNDL1") + struct.pack("<I", len(codes))
+    for code in codes:
+        blob += struct.pack("<I", len(code)) + code
+    blob += ops_blob
+    with open(path, "wb") as f:
+        f.write(bytes(blob))
+    return plans_written
+
+
+OPS_LIBRARY = hip.LIB_PATH.parent / "libneptune_ops.so"
 
 
 def stats(qualname: str) -> dict:

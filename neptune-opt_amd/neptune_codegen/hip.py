@@ -19,7 +19,8 @@ CACHE_DIR = PACKAGE_DIR / "_codeobj"
 
 NEP_OK = 0
 EXPORTED = ("nep_abi_version", "nep_last_error", "nep_compile", "nep_compile_code_object",
-            "nep_free", "nep_get_kernel", "nep_launch", "nep_launch_packed", "nep_device_arch")
+            "nep_free", "nep_module_load", "nep_get_kernel", "nep_launch", "nep_launch_packed",
+            "nep_device_arch")
 
 _lock = threading.Lock()
 _lib = None
@@ -155,10 +156,12 @@ class Kernel:
     kernarg segment uses) and launched in one library call.  Out-of-range values raise
     instead of wrapping."""
 
-    __slots__ = ("handle", "name", "argtypes", "block", "lds", "_packer", "pointer_offsets")
+    __slots__ = ("handle", "name", "argtypes", "block", "lds", "_packer", "pointer_offsets",
+                 "program")
 
     def __init__(self, handle: int, name: str, argtypes: tuple, block: int, lds: int = 0):
         self.handle, self.name, self.argtypes, self.block, self.lds = handle, name, argtypes, block, lds
+        self.program = None     # the Program whose module holds it (set by Program.kernel)
         try:
             codes = "".join(_ARG_CODES[t] for t in argtypes)
         except KeyError as error:
@@ -241,8 +244,16 @@ class Program:
                 module = load_module(self.source, self.name, self.options)
                 self._modules[device] = module
             k = Kernel(get_kernel(module, kernel_name), kernel_name, argtypes, block)
+            k.program = self
         self._kernels[key] = k
         return k
+
+    def code_object(self) -> bytes:
+        """The unit's gfx950 code object (from the on-disk cache, compiled if absent)."""
+        path = _cache_file(self.source, self.options)
+        if not (path.exists() and path.stat().st_size > 0):
+            compile_code_object(self.source, self.name, self.options)
+        return path.read_bytes()
 
     def precompile(self) -> int:
         """Fill the on-disk code-object cache (no GPU needed)."""

@@ -26,6 +26,29 @@ def test_library_exports_every_declared_symbol():
     assert lib.nep_abi_version() == 2
 
 
+def test_ops_library_exports_its_declared_symbol(tmp_path):
+    """libneptune_ops.so exports what include/neptune_ops.h declares; the C entry point reports
+    a damaged bundle through its error buffer (no GPU is touched before the magic check)."""
+    from neptune_codegen import dispatch
+
+    header = HEADER.parent / "neptune_ops.h"
+    names = sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(nep_\w+)\(", header.read_text(), re.M)))
+    assert names == ["nep_ops_load_bundle"]
+    import torch  # noqa: F401 -- the library resolves against torch's libraries
+
+    lib = ctypes.CDLL(str(dispatch.OPS_LIBRARY))
+    fn = lib.nep_ops_load_bundle
+    fn.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]
+    fn.restype = ctypes.c_int
+    bad = tmp_path / "bad.nepb"
+    bad.write_bytes(b"not a bundle at all")
+    err = ctypes.create_string_buffer(256)
+    assert fn(str(bad).encode(), err, len(err)) == -1
+    assert b"bad magic" in err.value
+    assert fn(str(tmp_path / "missing.nepb").encode(), err, len(err)) == -1
+    assert b"cannot open" in err.value
+
+
 def test_compile_code_object_and_error_reporting():
     lib = hip.load_library()
     ok = 'extern "C" __global__ void k(float* x) { x[threadIdx.x] *= 2.0f; }'

@@ -159,3 +159,67 @@ def test_cpu_backend_grad_goes_through_the_original_autograd_kernel():
     with torch.no_grad():
         assert not op(x).requires_grad
     assert dispatch.stats(name)["replays"] == 1
+
+
+# ---------------------------------------------------------------- launch-plan bundles
+import struct  # noqa: E402
+
+
+def _bundle(ops, codes=()):
+    """Bytes of a bundle in libneptune_ops' format (see nep_ops.cpp)."""
+    def s(text):
+        data = text.encode()
+        return struct.pack("<I", len(data)) + data
+
+    blob = b"NEPBNDL1" + struct.pack("<I", len(codes))
+    for code in codes:
+        blob += struct.pack("<I", len(code)) + code
+    blob += struct.pack("<I", len(ops))
+    for qualname, arguments, n_inputs, plans in ops:
+        blob += s(qualname) + s(arguments) + struct.pack("<II", n_inputs, len(plans))
+        for key, buffers in plans:
+            blob += struct.pack("<I", len(key)) + struct.pack(f"<{len(key)}q", *key)
+            blob += struct.pack("<I", len(buffers))
+            for code, sizes, strides in buffers:
+                blob += struct.pack("<iI", code, len(sizes)) + struct.pack(f"<{len(sizes)}q", *sizes)
+                blob += struct.pack(f"<{len(strides)}q", *strides)
+            blob += struct.pack("<I", 0)                 # no launches
+    return blob
+
+
+def _load_ops_library():
+    torch.ops.load_library(str(dispatch.OPS_LIBRARY))
+    return torch.ops.neptune_bundle.load
+
+
+def test_bundle_loader_defines_operators_once(tmp_path):
+    load = _load_ops_library()
+    path = tmp_path / "ok.nepb"
+    plan = ([6, 0, 2, 4, 8, 8, 1, 0], [(6, [4], [1])])
+    path.write_bytes(_bundle([("neptune_bundle_test::rows", "(Tensor x) -> Tensor", 1, [plan])]))
+    assert load(str(path)) == 1
+    dump = torch._C._dispatch_dump("neptune_bundle_test::rows")
+    assert "CUDA: registered at" in dump and "nep_ops.cpp" in dump, dump
+    assert str(torch._C._get_schema("neptune_bundle_test::rows", "")).endswith("(Tensor x) -> Tensor")
+    assert load(str(path)) == 0                          # already defined: left as it is
+
+
+@pytest.mark.parametrize("mutate, needle", [
+    (lambda b: b"NOTABNDL" + b[8:], "bad magic"),
+    (lambda b: b[:-5], "truncated"),
+    (lambda b: b + b"\0", "trailing"),
+])
+def test_bundle_loader_refuses_damaged_files(tmp_path, mutate, needle):
+    load = _load_ops_library()
+    good = _bundle([("neptune_bundle_test::damaged", "(Tensor x) -> Tensor", 1,
+                     [([6, 0, 1, 4, 1, 0], [(6, [], [])])])])
+    path = tmp_path / "bad.nepb"
+    path.write_bytes(mutate(good))
+    with pytest.raises(RuntimeError, match=needle):
+        load(str(path))
+
+
+def test_export_bundle_needs_recorded_plans(tmp_path):
+    op = torch_op.op_handle("logsumexp")
+    with pytest.raises(ValueError, match="no recorded launch plan"):
+        dispatch.export_bundle(tmp_path / "x.nepb", [op._schema.name + "_never_run"])

@@ -124,3 +124,66 @@ def test_compile_best_packages_measures_and_decides(tmp_path):
     runner = torch._inductor.aoti_load_package(choice.package_path)
     for g, w in zip(runner(x), model(x)):
         torch.testing.assert_close(g, w, rtol=1e-3, atol=1e-4)
+
+
+BUNDLE_CHILD = r"""
+import sys, torch
+ops_library, bundle, package, data = sys.argv[1:5]
+torch.ops.load_library(ops_library)
+defined = torch.ops.neptune_bundle.load(bundle)
+assert defined >= 1, defined
+import torch._inductor.codecache  # noqa: F401 -- aoti_load_package reads it, a fresh process lacks it
+runner = torch._inductor.aoti_load_package(package)
+d = torch.load(data, weights_only=True)
+got = runner(d["x"].to("cuda:0"))
+got = got[0] if isinstance(got, (tuple, list)) else got
+torch.cuda.synchronize()
+assert torch.equal(got.cpu(), d["want"]), (got.cpu() - d["want"]).abs().max()
+leaked = sorted(m for m in sys.modules if m.split(".")[0] in ("neptune_codegen", "neptune_opt", "neptune_recognize"))
+assert not leaked, leaked
+print("bundle child ok, operators defined:", defined, flush=True)
+"""
+
+
+@pytest.mark.timeout(600)
+def test_fused_package_runs_from_a_bundle_without_the_python_package(tmp_path):
+    """A fused AOTI package plus a launch-plan bundle run in a fresh process that never imports
+    neptune: libneptune_ops defines the operators and replays the bundled plans; the result is
+    bit-identical to the exporting process's run of the same package."""
+    import subprocess
+    import sys
+
+    from neptune_codegen import dispatch
+
+    dev = _dev()
+
+    class Model(torch.nn.Module):
+        def forward(self, x):
+            return torch.log_softmax(x, dim=-1), torch.logsumexp(x.float(), dim=-1)
+
+    x = (4 * torch.randn(300, 4096, generator=torch.Generator().manual_seed(31))).bfloat16().to(dev)
+    model = Model().eval()
+    ep = torch.export.export(model, (x,))
+    report = neptune_opt.apply(ep, verify_with=(model, (x,)), experimental_log_softmax=True,
+                               max_ulps=2)
+    _say(report.summary())
+    assert report.verified is True and len(report.fusions) == 2
+    ops = _neptune_ops(ep)
+    _say("fused graph ops:", ops)
+    package = str(tmp_path / "fused.pt2")
+    torch._inductor.aoti_compile_and_package(ep, package_path=package)
+    runner = torch._inductor.aoti_load_package(package)
+    want = runner(x)
+    torch.cuda.synchronize()
+    qualnames = [o.rsplit(".", 1)[0].replace(".", "::", 1) for o in ops]
+    bundle = str(tmp_path / "fused.nepb")
+    plans = dispatch.export_bundle(bundle, qualnames)
+    _say("bundle plans:", plans, "size:", (tmp_path / "fused.nepb").stat().st_size)
+    assert plans >= len(qualnames)      # every layout this process ran for these operators
+    data = str(tmp_path / "data.pt")
+    torch.save({"x": x.cpu(), "want": want[0].cpu()}, data)
+    # the package returns both outputs; the child checks the first (the readout)
+    proc = subprocess.run([sys.executable, "-c", BUNDLE_CHILD, str(dispatch.OPS_LIBRARY), bundle,
+                           package, data], capture_output=True, text=True, timeout=300)
+    _say(proc.stdout[-2000:], proc.stderr[-3000:])
+    assert proc.returncode == 0 and "bundle child ok" in proc.stdout
