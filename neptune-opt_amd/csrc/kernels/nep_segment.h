@@ -178,4 +178,86 @@ __device__ __forceinline__ void segment_generic(const typename St::T* __restrict
   St::store(out + seg * channels + c, segment_readout<St, MEAN, INIT_NONE>(acc, valid, start, end));
 }
 
+// ---------------------------------------------------------------- lengths -> spans
+// spans[0] = 0, spans[i + 1] = lengths[0] + ... + lengths[i] in int64: the reference's
+// cat(0, cumsum(lengths)) (torch_op.py:370-387).  Two launches over blocks of kSpanBlock
+// lengths: the block sums, then each block scans itself on top of the sum of the blocks before
+// it (no inter-workgroup synchronisation).  Bad lengths are not judged here: the segment
+// kernel's span checks see the resulting spans.
+constexpr int kSpanThreads = 256;
+constexpr int kSpanPer = 4;
+constexpr i64 kSpanBlock = (i64)kSpanThreads * kSpanPer;
+
+__device__ __forceinline__ i64 wave_sum_i64(i64 v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+// Sum over the workgroup, returned to every thread.
+__device__ __forceinline__ i64 block_sum_i64(i64 v, i64* lds) {
+  v = wave_sum_i64(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) lds[wave] = v;
+  __syncthreads();
+  i64 total = 0;
+#pragma unroll
+  for (int w = 0; w < kSpanThreads / 64; ++w) total += lds[w];
+  return total;
+}
+
+// Exclusive scan over the workgroup's threads (in thread order).
+__device__ __forceinline__ i64 block_exclusive_i64(i64 v, i64* lds) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  i64 inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const i64 o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  __syncthreads();
+  if (lane == 63) lds[wave] = inc;
+  __syncthreads();
+  i64 before = 0;
+  for (int w = 0; w < wave; ++w) before += lds[w];
+  return before + inc - v;
+}
+
+template <class L>
+__device__ __forceinline__ void spans_block_sums(const L* __restrict__ lengths, i64 n,
+                                                 i64* __restrict__ sums) {
+  __shared__ i64 lds[kSpanThreads / 64];
+  const i64 base = (i64)blockIdx.x * kSpanBlock + (i64)threadIdx.x * kSpanPer;
+  i64 s = 0;
+#pragma unroll
+  for (int k = 0; k < kSpanPer; ++k)
+    if (base + k < n) s += (i64)lengths[base + k];
+  s = block_sum_i64(s, lds);
+  if (threadIdx.x == 0) sums[blockIdx.x] = s;
+}
+
+template <class L>
+__device__ __forceinline__ void spans_scan(const L* __restrict__ lengths, i64 n,
+                                           const i64* __restrict__ sums,
+                                           i64* __restrict__ spans) {
+  __shared__ i64 lds[kSpanThreads / 64];
+  i64 before = 0;
+  for (i64 b = threadIdx.x; b < (i64)blockIdx.x; b += kSpanThreads) before += sums[b];
+  before = block_sum_i64(before, lds);
+  const i64 base = (i64)blockIdx.x * kSpanBlock + (i64)threadIdx.x * kSpanPer;
+  i64 run[kSpanPer];
+  i64 acc = 0;
+#pragma unroll
+  for (int k = 0; k < kSpanPer; ++k) {
+    acc += base + k < n ? (i64)lengths[base + k] : 0;
+    run[k] = acc;
+  }
+  const i64 offset = before + block_exclusive_i64(acc, lds);
+#pragma unroll
+  for (int k = 0; k < kSpanPer; ++k)
+    if (base + k < n) spans[base + k + 1] = offset + run[k];
+  if (blockIdx.x == 0 && threadIdx.x == 0) spans[0] = 0;
+}
+
 }  // namespace nep

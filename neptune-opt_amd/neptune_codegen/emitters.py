@@ -482,6 +482,26 @@ def emit_segment_source(name: str, *, initial=None, offsets=False, plan="serial"
     return "\n".join(parts)
 
 
+SPAN_BLOCK = 256 * 4           # lengths per workgroup of the spans kernels (nep_segment.h)
+
+
+def emit_segment_spans_source() -> str:
+    """hiprtc unit of the lengths -> spans prefix sum (int32 and int64 lengths)."""
+    parts = ["// AUTO-GENERATED by neptune_codegen (HIP emitter) -- do not edit.\n"
+             "// segment lengths -> int64 spans [0, cumsum(lengths)]\n",
+             kernel_header("nep_device.h", "nep_segment.h")]
+    for tag, ctype in (("i32", "int"), ("i64", "long long")):
+        parts.append(
+            f'extern "C" __global__ void __launch_bounds__(256) segment_spans_sums_{tag}('
+            "const void* lengths, long long n, long long* sums) {\n"
+            f"  nep::spans_block_sums<{ctype}>((const {ctype}*)lengths, n, sums);\n}}\n")
+        parts.append(
+            f'extern "C" __global__ void __launch_bounds__(256) segment_spans_scan_{tag}('
+            "const void* lengths, long long n, const long long* sums, long long* spans) {\n"
+            f"  nep::spans_scan<{ctype}>((const {ctype}*)lengths, n, sums, spans);\n}}\n")
+    return "\n".join(parts)
+
+
 def segment_kernel_name(name: str, var: SegmentVariant) -> str:
     return f"{name}_{var.tag()}"
 

@@ -384,16 +384,45 @@ DESCRIPTOR_MESSAGE = ("segment descriptor is invalid: lengths must be nonnegativ
                       "bounds and be monotonic")
 
 
+_SPANS_PROGRAM = None
+
+
+def _spans_program() -> hip.Program:
+    global _SPANS_PROGRAM
+    with _lock:
+        if _SPANS_PROGRAM is None:
+            from neptune_codegen.emitters import emit_segment_spans_source
+
+            _SPANS_PROGRAM = hip.Program(emit_segment_spans_source(), "segment_spans.hip",
+                                         BASE_OPTIONS)
+        return _SPANS_PROGRAM
+
+
 def _device_spans(data, segments, *, offsets):
     """[start, end) boundaries for the fused-validation launch: offsets as given, lengths as an
-    int64 prefix sum (the same values `_segment_spans` builds); no asserts here."""
+    int64 prefix sum (the same values `_segment_spans` builds) by two HIP launches -- block
+    sums, then a per-block scan on top of the preceding blocks; no asserts here (the segment
+    kernel checks the spans)."""
     import torch
+
+    from neptune_codegen.emitters import SPAN_BLOCK
 
     if offsets:
         return segments
-    spans = torch.empty(segments.shape[0] + 1, dtype=torch.int64, device=segments.device)
-    spans[:1].zero_()
-    torch.cumsum(segments, dim=0, dtype=torch.int64, out=spans[1:])
+    lengths = segments.contiguous()
+    n = lengths.shape[0]
+    spans = torch.empty(n + 1, dtype=torch.int64, device=segments.device)
+    nblocks = (n + SPAN_BLOCK - 1) // SPAN_BLOCK
+    sums = hip.scratch(torch.empty(nblocks, dtype=torch.int64, device=segments.device))
+    tag = "i32" if lengths.dtype == torch.int32 else "i64"
+    device = segments.device.index if segments.device.index is not None else torch.cuda.current_device()
+    prog = _spans_program()
+    stream = hip.current_stream(segments.device)
+    prog.kernel(f"segment_spans_sums_{tag}", (hip.PTR, hip.I64, hip.PTR), 256, device).launch(
+        (nblocks,), (lengths.data_ptr(), n, sums.data_ptr()), stream)
+    prog.kernel(f"segment_spans_scan_{tag}", (hip.PTR, hip.I64, hip.PTR, hip.PTR), 256,
+                device).launch((nblocks,), (lengths.data_ptr(), n, sums.data_ptr(),
+                                            spans.data_ptr()), stream)
     return spans
 
 

@@ -234,3 +234,22 @@ def test_segment_fused_descriptor_check_matches_reference_asserts():
             if reference_ok:
                 want = R.segment_reference(data, seg, "sum", offsets=is_offsets, unsafe=unsafe)
                 _bits_equal(out.cpu(), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_lengths_prefix_sum_kernel_is_exact(dtype):
+    """The HIP lengths -> spans scan equals cat(0, cumsum(lengths)) exactly, across block
+    boundaries (1024 lengths per workgroup) and with zero and very large lengths."""
+    from neptune_codegen.torch_op import _device_spans
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(41)
+    for n in (1, 5, 1023, 1024, 1025, 65536, 1_000_003):
+        lengths = torch.randint(0, 201, (n,), generator=g).to(dtype)
+        lengths[::7] = 0
+        if dtype == torch.int64:
+            lengths[n // 2] = 1 << 40
+        print(f"spans scan {dtype} n={n}", flush=True)
+        got = _device_spans(None, lengths.to(dev), offsets=False).cpu()
+        want = torch.cat([torch.zeros(1, dtype=torch.int64), lengths.to(torch.int64).cumsum(0)])
+        assert got.dtype == torch.int64 and torch.equal(got, want)
