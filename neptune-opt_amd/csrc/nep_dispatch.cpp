@@ -52,6 +52,9 @@ struct Stats {
   int64_t replays = 0, python_calls = 0, plans = 0;
 };
 
+// Plans kept per operator; later layouts keep calling the Python body (correct, slower).
+constexpr size_t kMaxPlans = 1024;
+
 class PlanKernel final : public c10::OperatorKernel {
  public:
   PlanKernel(int n_inputs, c10::DeviceType device_type, PyObject* body,
@@ -78,7 +81,12 @@ class PlanKernel final : public c10::OperatorKernel {
     at::Tensor out;
     {
       py::gil_scoped_acquire gil;
-      const bool record = keyed && !plan;
+      bool full;
+      {
+        std::lock_guard<std::mutex> guard(mu_);
+        full = cache_.size() >= kMaxPlans;
+      }
+      const bool record = keyed && !plan && !full;
       py::tuple call(n_inputs_ + 1);
       call[0] = py::bool_(record);
       for (int i = 0; i < n_inputs_; ++i) call[i + 1] = py::cast(args[i].toTensor());
@@ -113,10 +121,12 @@ class PlanKernel final : public c10::OperatorKernel {
     if (spec.is_none()) return plan;  // known key, Python only
     py::tuple t = spec.cast<py::tuple>();
     for (py::handle b : t[0].cast<py::tuple>()) {
-      py::tuple bt = b.cast<py::tuple>();
-      at::Tensor example = bt[0].cast<at::Tensor>();
-      plan->buffers.push_back(
-          {example.sizes().vec(), example.strides().vec(), example.scalar_type()});
+      py::tuple bt = b.cast<py::tuple>();   // (scalar type code, sizes, strides)
+      plan->buffers.push_back({bt[1].cast<std::vector<int64_t>>(),
+                               bt[2].cast<std::vector<int64_t>>(),
+                               static_cast<c10::ScalarType>(bt[0].cast<int>())});
+      if (plan->buffers.back().sizes.size() != plan->buffers.back().strides.size())
+        return std::make_shared<Plan>();
     }
     for (py::handle l : t[1].cast<py::tuple>()) {
       py::tuple lt = l.cast<py::tuple>();

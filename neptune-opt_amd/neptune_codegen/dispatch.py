@@ -20,7 +20,9 @@ A call whose body launches with a pointer that is neither an input nor a recorde
 (an input copied by reshape/contiguous, say) leaves no plan, and its key keeps using Python.
 Bodies installed here must launch only through `hip.Kernel` and allocate scratch through
 `hip.scratch`; the segment operators (device-side prefix sums and asserts) are not installed.
-Plans are per process; `clear()` drops them (after replacing the launch table, for example).
+Plans are per process, at most MAX_PLANS (1024) per operator -- later layouts keep using the
+Python body -- and hold only metadata; `clear()` drops them (after replacing the launch table,
+for example).
 """
 from __future__ import annotations
 
@@ -32,6 +34,7 @@ from neptune_codegen import hip
 
 _lock = threading.Lock()
 _module = None
+MAX_PLANS = 1024      # per operator; later layouts keep using the Python body
 # qualname -> {"arguments": schema text after the name, "n_inputs": int,
 #              "plans": {key tuple: (plan, kernels)}}: what export_bundle writes
 _RECORDED: dict = {}
@@ -93,7 +96,10 @@ def plan_of(recorder: hip.Recorder, inputs: tuple, outputs: tuple):
                 return None
             patches.append((offset, source))
         launches.append((kernel.handle, grid, kernel.block, kernel.lds, image, tuple(patches)))
-    return tuple((b,) for b in buffers), tuple(launches)
+    # buffers by metadata only: a plan must not keep the first call's tensors alive
+    code = extension().dtype_code
+    return (tuple((code(b), tuple(b.shape), tuple(b.stride())) for b in buffers),
+            tuple(launches))
 
 
 def install(qualname: str, n_inputs: int, body, *, backend: str = "CUDA") -> None:
@@ -125,7 +131,8 @@ def install(qualname: str, n_inputs: int, body, *, backend: str = "CUDA") -> Non
             key = ext.key_of(list(inputs))
             if key is not None:
                 with _lock:
-                    entry["plans"][tuple(key)] = (plan, [k for k, *_ in recorder.launches])
+                    if len(entry["plans"]) < MAX_PLANS:
+                        entry["plans"][tuple(key)] = (plan, [k for k, *_ in recorder.launches])
         return out, plan
 
     def grad_body(*inputs):
@@ -173,10 +180,10 @@ def export_bundle(path, qualnames=None) -> int:
         for key, ((buffers, launches), kernels) in entry["plans"].items():
             ops_blob += struct.pack("<I", len(key)) + struct.pack(f"<{len(key)}q", *key)
             ops_blob += struct.pack("<I", len(buffers))
-            for (tensor,) in buffers:
-                ops_blob += struct.pack("<iI", ext.dtype_code(tensor), tensor.dim())
-                ops_blob += struct.pack(f"<{tensor.dim()}q", *tensor.shape)
-                ops_blob += struct.pack(f"<{tensor.dim()}q", *tensor.stride())
+            for dtype_code, sizes, strides in buffers:
+                ops_blob += struct.pack("<iI", dtype_code, len(sizes))
+                ops_blob += struct.pack(f"<{len(sizes)}q", *sizes)
+                ops_blob += struct.pack(f"<{len(strides)}q", *strides)
             ops_blob += struct.pack("<I", len(launches))
             for (_handle, grid, block, lds, image, patches), kernel in zip(launches, kernels):
                 program = kernel.program

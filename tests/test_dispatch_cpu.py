@@ -56,7 +56,9 @@ def test_plan_maps_pointers_to_inputs_and_buffers():
     args = (x.data_ptr(), out.data_ptr(), scratch.data_ptr(), 4)
     rec = _recorded([(k, (3, 1, 1), k._packer.pack(*args), args)], [scratch])
     buffers, launches = dispatch.plan_of(rec, (x,), (out,))
-    assert [b[0] is t for b, t in zip(buffers, (out, scratch))] == [True, True]
+    code = dispatch.extension().dtype_code
+    assert buffers == ((code(out), (4,), (1,)), (code(scratch), (4, 2), (2, 1)))
+    assert not any(isinstance(v, torch.Tensor) for b in buffers for v in b)   # metadata only
     handle, grid, block, lds, image, patches = launches[0]
     assert grid == (3, 1, 1) and block == 64
     assert patches == ((0, 0), (8, -1), (16, -2))
@@ -223,3 +225,18 @@ def test_export_bundle_needs_recorded_plans(tmp_path):
     op = torch_op.op_handle("logsumexp")
     with pytest.raises(ValueError, match="no recorded launch plan"):
         dispatch.export_bundle(tmp_path / "x.nepb", [op._schema.name + "_never_run"])
+
+
+def test_cpu_backend_caps_plans_per_operator():
+    op, name = _cpu_op("capped", _rows_body)
+    for n in range(1, dispatch.MAX_PLANS + 1):
+        op(torch.empty(n, 3))
+    assert dispatch.stats(name)["plans"] == dispatch.MAX_PLANS
+    extra = torch.empty(dispatch.MAX_PLANS + 7, 3)
+    op(extra)
+    op(extra)
+    s = dispatch.stats(name)
+    assert s["plans"] == dispatch.MAX_PLANS and s["replays"] == 0
+    assert s["python_calls"] == dispatch.MAX_PLANS + 2
+    op(torch.empty(1, 3))                                   # an early layout still replays
+    assert dispatch.stats(name)["replays"] == 1
