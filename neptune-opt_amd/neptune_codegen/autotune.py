@@ -12,7 +12,10 @@ A fold's launch configuration is `(BLOCK, num_warps)`, as in the reference
 
 Shapes with no measured entry use `default_config`, which sizes the tile to the row rather
 than using one fixed block: short rows get a few lanes each (many rows per wavefront), long
-rows a multi-wavefront workgroup.  Measured MI355X deviations live in launch_table.py.
+rows a multi-wavefront workgroup.  Measured MI355X deviations live in launch_table.py, keyed
+by (rows class, width bucket) as in the reference, or by (rows class, width bucket, dtype)
+where the best tile differs between storage types (BLOCK counts elements, so the same BLOCK
+is a different tile in bytes); a dtype key wins over the plain one.
 
 Operator identity (`op_key`, `parameter_tag`, `parameter_identity`) is the reference's scheme
 (autotune.py:392-432) unchanged: registered op names must stay stable across backends.
@@ -28,6 +31,12 @@ MAX_UNROLL = 8
 # on MI355X, bf16 logsumexp, cold cache: 32000 wide 157.9 vs 162.6 us, 65536 wide 159.0 vs
 # 164.3 us, 262144 wide 161.2 vs 169.3 us; at 16384 wide 8 slots lose (174.6 vs 163.8 us).
 WIDE_16BIT_ROW = 24576
+# 16-bit rows from 2048 up to that width walk the row in two tiles of half its width on two
+# waves.  Measured on MI355X, logsumexp, 16384 rows, cold cache, against the full-width tile on
+# four waves: bf16 2048 wide 13.6 vs 14.1 us, 4096 22.9 vs 24.0, 8192 41.9 vs 46.7, 16384
+# 79.4 vs 84.8; fp16 4096 23.2 vs 24.6, 8192 42.3 vs 47.7, 16384 79.7 vs 86.2.  fp32 keeps the
+# full tile (within 2% of the best candidate at every width).
+MID_16BIT_ROW = 2048
 CANDIDATES: tuple = tuple((b, w) for b in (128, 256, 512, 1024, 2048, 4096, 8192, 16384)
                           for w in (1, 2, 4, 8))
 DEFAULT: tuple = (1024, 4)
@@ -99,6 +108,11 @@ def shape_key(rows, ncols) -> tuple:
     return rows_class(rows), ncols_bucket(ncols)
 
 
+def dtype_name(dtype) -> str:
+    """'float32' / 'bfloat16' / 'float16' (the optional third element of a table key)."""
+    return str(dtype).replace("torch.", "")
+
+
 def _valid(body) -> dict:
     return {tuple(k): tuple(v) for k, v in (body or {}).items() if tuple(v) in CANDIDATES}
 
@@ -151,6 +165,8 @@ def default_config(rows, ncols, dtype=None) -> tuple:
     if dtype is not None and vec_of(dtype) == 8 and ncols >= WIDE_16BIT_ROW:
         return step * 512, 4
     tile = 1 << max(0, (max(ncols, 1) - 1).bit_length())
+    if dtype is not None and vec_of(dtype) == 8 and ncols >= MID_16BIT_ROW:
+        return tile // 2, 2
     block = max(step * 4, min(tile, step * 256))
     return block, 4
 
@@ -193,7 +209,10 @@ def _best_config(rows, ncols, dtype, device, device_name, verbose) -> tuple:
     if device_name is None:
         device_name = device_name_of(device)
     machine = machine_key(device_name) if device_name else ""
-    cfg = table(machine).get(shape_key(rows, ncols))
+    entries = table(machine)
+    key = shape_key(rows, ncols)
+    cfg = entries.get(key + (dtype_name(dtype),)) if dtype is not None else None
+    cfg = entries.get(key) if cfg is None else cfg
     source = "measured"
     if cfg is None:
         cfg, source = default_config(rows, ncols, dtype), "default"

@@ -28,7 +28,10 @@ def _fold_programs():
     for name in supported():
         params = {**param_defaults(name), **({"eps": 1e-6} if name == "rmsnorm_max" else {})}
         prog = compile_skeleton(name, params)
-        out.append(prog.program(_fold_variant(x2, 4096, block, warps, resident=prog.sk.two_pass)))
+        sk = prog.sk
+        out.append(prog.program(_fold_variant(x2, 4096, block, warps, resident=sk.two_pass,
+                                              merge_heavy=not sk.is_log and not sk.two_pass,
+                                              heavy_phi=prog.heavy_phi)))
     from neptune_codegen.template import compile_readout
 
     xw = torch.empty((16384, 32000), device="meta", dtype=torch.bfloat16)
