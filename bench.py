@@ -415,9 +415,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-folds", action="store_true", help="skip the per-configuration table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--pmc-probe", action="store_true",
-                    help="only run the dominant kernel and a 256 MiB copy (3x each), for "
-                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs and their calibration")
+    ap.add_argument("--pmc-probe", nargs="?", const="dominant", default=None,
+                    choices=("dominant", "all"),
+                    help="only run the dominant kernel (or, with 'all', also RMSNorm, segment "
+                         "sum, the log-softmax readout and the two-pass variance) and a 256 MiB "
+                         "copy, 3x each, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs and "
+                         "their calibration")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="only time a plain streaming-read kernel at the fold input sizes (the "
                          "practical ceiling the folds are compared against), then exit")
@@ -443,8 +446,24 @@ def main():
         x = (4 * torch.randn(16384, 32000, generator=seeded(1))).bfloat16().to(dev)
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)   # 256 MiB
         dst = torch.empty_like(src)
+        calls = [lambda: CG.run("logsumexp", x)]
+        if args.pmc_probe == "all":
+            g3 = seeded(3)
+            x3 = torch.randn(32768, 4096, generator=g3).bfloat16().to(dev)
+            gamma = (1 + 0.1 * torch.randn(4096, generator=g3)).bfloat16().to(dev)
+            g4 = seeded(4)
+            lengths = torch.poisson(torch.full((65536,), 20.0), generator=g4).clamp(0, 200).to(torch.int32)
+            data = torch.randn(int(lengths.sum()), 128, generator=g4).half().to(dev)
+            offsets = torch.cat([torch.zeros(1, dtype=torch.int32),
+                                 lengths.cumsum(0).to(torch.int32)]).to(dev)
+            xv = torch.randn(16384, 4096, generator=seeded(12)).to(dev)
+            calls += [lambda: CG.run_rms_norm(x3, gamma, eps=1e-6),
+                      lambda: CG.run_segment_pool(data, offsets, reduce="sum", offsets=True),
+                      lambda: CG.run_log_softmax(x),
+                      lambda: CG.run("variance", xv)]
         for _ in range(3):
-            CG.run("logsumexp", x)
+            for call in calls:
+                call()
             dst.copy_(src)
         torch.cuda.synchronize()
         log("[bench] pmc probe done")
