@@ -138,19 +138,43 @@ __device__ __forceinline__ void store16(void* p, const u32x4& w) {
 // wavefront.  Steps 1 and 2 are exact xor exchanges (DPP quad_perm); 4 and 8 use the DPP
 // half-row / row mirrors, which pair every lane with a lane of the partner group -- valid for
 // butterfly reductions because after the smaller steps every lane of a group holds the same
-// value.  16 is ds_swizzle (xor 16 inside 32 lanes) and 32 crosses the halves with
-// ds_bpermute.  All lanes of the wavefront must be active.
+// value.  16 and 32 are exact xor exchanges through gfx950's v_permlane16_swap /
+// v_permlane32_swap (VALU, no LDS round trip): swapping a value with itself leaves every lane
+// holding the pair (lower, upper) of its 16- or 32-lane partner group, verified on the GPU:
+// permlane16_swap(v, v) = {v[l & ~16], v[l | 16]}, permlane32_swap(v, v) = {v[l & 31],
+// v[(l & 31) | 32]}.  All lanes of the wavefront must be active.
 template <int S>
 __device__ __forceinline__ u32 partner_u32(u32 v) {
   if constexpr (S == 1) return (u32)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
   else if constexpr (S == 2) return (u32)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
   else if constexpr (S == 4) return (u32)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);
   else if constexpr (S == 8) return (u32)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);
-  else if constexpr (S == 16) return (u32)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);
   else {
-    static_assert(S == 32, "partner step must be 1..32");
-    const int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0));
-    return (u32)__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, (int)v);
+    static_assert(S == 16 || S == 32, "partner step must be 1..32");
+    const u32 lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0));
+    if constexpr (S == 16) {
+      const auto p = __builtin_amdgcn_permlane16_swap(v, v, true, false);
+      return (lane & 16u) ? p[0] : p[1];
+    } else {
+      const auto p = __builtin_amdgcn_permlane32_swap(v, v, true, false);
+      return (lane & 32u) ? p[0] : p[1];
+    }
+  }
+}
+
+// Both members of the S-lane partner pair (lower group's value, upper group's value), the same
+// in every lane of the pair: reductions combine them in one order, bit-identical across lanes.
+template <int S>
+__device__ __forceinline__ void pair_u32(u32 v, u32& lo, u32& hi) {
+  static_assert(S == 16 || S == 32, "pair exchange is for steps 16 and 32");
+  if constexpr (S == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, true, false);
+    lo = p[0];
+    hi = p[1];
+  } else {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, true, false);
+    lo = p[0];
+    hi = p[1];
   }
 }
 template <int S>
@@ -160,14 +184,27 @@ __device__ __forceinline__ int partner(int v) { return (int)partner_u32<S>((u32)
 
 // Sum / max over aligned groups of G lanes (G a power of two <= 64); every lane of the group
 // receives the result.
+template <int S>
+__device__ __forceinline__ float pair_sum(float v) {
+  u32 lo, hi;
+  pair_u32<S>(as_u32(v), lo, hi);
+  return as_f32(lo) + as_f32(hi);
+}
+template <int S>
+__device__ __forceinline__ float pair_max(float v) {
+  u32 lo, hi;
+  pair_u32<S>(as_u32(v), lo, hi);
+  return __builtin_fmaxf(as_f32(lo), as_f32(hi));
+}
+
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
   if constexpr (G >= 2) v += partner<1>(v);
   if constexpr (G >= 4) v += partner<2>(v);
   if constexpr (G >= 8) v += partner<4>(v);
   if constexpr (G >= 16) v += partner<8>(v);
-  if constexpr (G >= 32) v += partner<16>(v);
-  if constexpr (G >= 64) v += partner<32>(v);
+  if constexpr (G >= 32) v = pair_sum<16>(v);
+  if constexpr (G >= 64) v = pair_sum<32>(v);
   return v;
 }
 template <int G>
@@ -176,8 +213,8 @@ __device__ __forceinline__ float group_max(float v) {
   if constexpr (G >= 4) v = __builtin_fmaxf(v, partner<2>(v));
   if constexpr (G >= 8) v = __builtin_fmaxf(v, partner<4>(v));
   if constexpr (G >= 16) v = __builtin_fmaxf(v, partner<8>(v));
-  if constexpr (G >= 32) v = __builtin_fmaxf(v, partner<16>(v));
-  if constexpr (G >= 64) v = __builtin_fmaxf(v, partner<32>(v));
+  if constexpr (G >= 32) v = pair_max<16>(v);
+  if constexpr (G >= 64) v = pair_max<32>(v);
   return v;
 }
 template <int G>

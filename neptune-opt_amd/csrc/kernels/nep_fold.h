@@ -104,25 +104,6 @@ __device__ __forceinline__ LogLane log_merge(const LogLane& A, const LogLane& B)
   return R;
 }
 
-template <int G>
-__device__ __forceinline__ LogLane log_group_merge(LogLane s) {
-#define NEP_LOG_STEP(S)                                                   \
-  {                                                                       \
-    LogLane o;                                                            \
-    o.m = partner<S>(s.m);                                                \
-    o.acc = partner<S>(s.acc);                                            \
-    o.flag = partner<S>(s.flag);                                          \
-    s = log_merge(s, o);                                                  \
-  }
-  if constexpr (G >= 2) NEP_LOG_STEP(1)
-  if constexpr (G >= 4) NEP_LOG_STEP(2)
-  if constexpr (G >= 8) NEP_LOG_STEP(4)
-  if constexpr (G >= 16) NEP_LOG_STEP(8)
-  if constexpr (G >= 32) NEP_LOG_STEP(16)
-  if constexpr (G >= 64) NEP_LOG_STEP(32)
-#undef NEP_LOG_STEP
-  return s;
-}
 
 // ---------------------------------------------------------------- tile access
 template <class St, int TPR, int UNROLL, bool VECTOR>
@@ -382,10 +363,20 @@ __device__ __forceinline__ LogLane log_row_lane(const typename St::T* row, i64 s
   return s;
 }
 
+// A row's lanes combine in two reductions instead of a tree of pairwise merges: the row max
+// first, then each lane moves its sum to it once (one exponential per lane instead of one per
+// tree level and partner) and the sums are added.  A lane with no finite value contributes 0;
+// NaN sums (a +inf element) stay NaN and send the row to the exact path as before.
 template <class F, int TPR>
 __device__ __forceinline__ LogLane log_row_combine(LogLane s, LogLane* lds) {
   typedef RowComm<TPR> RC;
-  s = log_group_merge<RC::G>(s);
+  {
+    const float row_m = group_max<RC::G>(s.m);
+    const float moved = (s.m == -kInf) ? 0.0f : s.acc * fast_exp(s.m - row_m);
+    s.acc = group_sum<RC::G>(moved);
+    s.m = row_m;
+    s.flag = group_or<RC::G>(s.flag);
+  }
   if constexpr (RC::WPR > 1) {
     const int wave = threadIdx.x >> 6, first = (wave / RC::WPR) * RC::WPR;
     if (lane_id() == 0) lds[wave] = s;
