@@ -433,7 +433,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; every fold is row/segment-parallel and "
-              "shards without communication (see DESIGN.md), so only --gpus 1 is run.",
+              "shards across GPUs without communication, so only --gpus 1 is run.",
               file=sys.stderr)
         sys.exit(2)
     import torch
