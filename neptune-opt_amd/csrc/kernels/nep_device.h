@@ -40,6 +40,27 @@ __device__ __forceinline__ float quot(float num, float den) {
   return (num * sc) * (1.0f / (den * sc));
 }
 
+// Repair slopes and biases (evaluated once per tile and once per merge, never per element) use
+// the hardware square root, reciprocal square root and reciprocal (v_sqrt_f32, v_rsq_f32,
+// v_rcp_f32: 1 ulp each), the precision class of the reference's Triton lowering, whose
+// tl.sqrt and fp32 division are not correctly rounded either.  Arguments outside
+// [2^-64, 2^64] are first scaled by an exact power of two, so the instructions never see a
+// denormal input or produce a denormal result; 0, inf and NaN keep their IEEE results.
+__device__ __forceinline__ float fsqrt(float x) {
+  const bool small = x < 0x1p-64f;
+  return __builtin_amdgcn_sqrtf(small ? x * 0x1p64f : x) * (small ? 0x1p-32f : 1.0f);
+}
+__device__ __forceinline__ float frsq(float x) {
+  const float sc = x < 0x1p-64f ? 0x1p64f : (x > 0x1p64f ? 0x1p-64f : 1.0f);
+  const float back = x < 0x1p-64f ? 0x1p32f : (x > 0x1p64f ? 0x1p-32f : 1.0f);
+  return __builtin_amdgcn_rsqf(x * sc) * back;
+}
+__device__ __forceinline__ float fquot(float num, float den) {
+  const float a = __builtin_fabsf(den);
+  const float sc = a < 0x1p-64f ? 0x1p64f : (a > 0x1p64f ? 0x1p-64f : 1.0f);
+  return (num * __builtin_amdgcn_rcpf(den * sc)) * sc;
+}
+
 // ---------------------------------------------------------------- storage dtypes
 // bf16 -> fp32 is exact (the high half of an fp32 pattern).  fp32 -> bf16 rounds to nearest
 // even.  f32_to_bf16_bits is the integer statement of that rounding (NaN -> the canonical

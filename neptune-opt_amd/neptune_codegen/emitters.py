@@ -167,9 +167,10 @@ def emit_fold_policy(sk: Skeleton, values: dict | None = None, *, struct_name: s
             term = to_hip(_marked(term_expr(sk)), {**bind, c_sym: "v", s2_sym: "den"},
                           shared=c_sym)
         a, b = repair_factor(sk), repair_bias(sk)
-        rho = to_hip(_marked(a), {**bind, s_sym: "q", s2_sym: "q2"})
+        rho = to_hip(_marked(a), {**bind, s_sym: "q", s2_sym: "q2"}, fast=True)
         has_bias = b != 0
-        beta = to_hip(_marked(b), {**bind, s_sym: "q", s2_sym: "q2"}) if has_bias else "0.0f"
+        beta = (to_hip(_marked(b), {**bind, s_sym: "q", s2_sym: "q2"}, fast=True) if has_bias
+                else "0.0f")
         fin_m = "nep::eff<Self>(m)" if floor else "m"
     finalize = to_hip(sk.finalize, {**bind, _FINAL_M: "m_", _FINAL_ACC: "acc"})
     return f"""struct {struct_name} {{

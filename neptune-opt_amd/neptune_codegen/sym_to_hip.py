@@ -11,6 +11,10 @@ lowering rules that carry numerical meaning are kept:
   * with `shared` given, a quotient whose denominator does not mention that symbol (a fold
     term's divisor fixed per tile) lowers to nep::quot, a multiply by one shared reciprocal;
   * x**(1/2) is sqrtf(x), x**(-1/2) is 1.0f / sqrtf(x), integer powers are products;
+  * with `fast` (repair slopes and biases, evaluated per tile and per merge, never per
+    element), x**(1/2), x**(-1/2) and quotients use the hardware instructions instead
+    (nep::fsqrt, nep::frsq, nep::fquot: 1 ulp each), the precision class of the reference's
+    Triton lowering (tl.sqrt and fp32 division, neither correctly rounded);
   * other fractional powers are allowed only for a provably positive base (exp2(log2(b) p));
   * numeric literals are rounded to fp32 once and written as exact hex-float literals.
 """
@@ -47,12 +51,16 @@ def _positive_base(base: sp.Expr) -> bool:
     return base.is_positive is True
 
 
-def to_hip(expr: sp.Expr, names: dict, shared: sp.Symbol | None = None) -> str:
+def to_hip(expr: sp.Expr, names: dict, shared: sp.Symbol | None = None,
+           fast: bool = False) -> str:
     """Render `expr` as an fp32 C++ expression; `names` maps symbols to source text.  With
-    `shared` (the per-element symbol), divisors free of it become shared reciprocals."""
+    `shared` (the per-element symbol), divisors free of it become shared reciprocals; with
+    `fast`, square roots and quotients use the 1-ulp hardware instructions."""
     expr = sp.sympify(expr)
 
     def divide(top: str, bottom: str, divisor: sp.Expr) -> str:
+        if fast:
+            return f"nep::fquot({top}, {bottom})"
         if shared is not None and not divisor.has(shared):
             return f"nep::quot({top}, {bottom})"
         return f"({top} / {bottom})"
@@ -84,7 +92,9 @@ def to_hip(expr: sp.Expr, names: dict, shared: sp.Symbol | None = None) -> str:
             numer, denom, divisor = [], [], sp.Integer(1)
             for factor in e.args:
                 base, ex = factor.as_base_exp()
-                if ex.is_Number and ex.is_negative:
+                if fast and ex == sp.Rational(-1, 2):
+                    numer.append(f"nep::frsq({rec(base)})")
+                elif ex.is_Number and ex.is_negative:
                     denom.append(rec(base ** (-ex)))
                     divisor = divisor * base ** (-ex)
                 else:
@@ -103,9 +113,9 @@ def to_hip(expr: sp.Expr, names: dict, shared: sp.Symbol | None = None) -> str:
                 prod = "(" + " * ".join([b] * abs(k)) + ")"
                 return prod if k > 0 else divide("1.0f", prod, base)
             if ex == sp.Rational(1, 2):
-                return f"sqrtf({rec(base)})"
+                return f"nep::fsqrt({rec(base)})" if fast else f"sqrtf({rec(base)})"
             if ex == sp.Rational(-1, 2):
-                return f"(1.0f / sqrtf({rec(base)}))"
+                return f"nep::frsq({rec(base)})" if fast else f"(1.0f / sqrtf({rec(base)}))"
             if _positive_base(base):
                 return f"exp2f(log2f({rec(base)}) * {rec(ex)})"
             raise TranslationError(f"fractional power of a base not proved positive: {e}")

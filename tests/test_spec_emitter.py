@@ -94,6 +94,13 @@ def test_translator_rules():
     assert CG.to_hip(sp.sqrt(x), names) == "sqrtf((x))"
     assert CG.to_hip(1 / sp.sqrt(x), names) == "(1.0f / sqrtf((x)))"
     assert CG.to_hip(CG._marked((x / y) ** 2), names) == "(((x) / (y)) * ((x) / (y)))"
+    # repair slopes: hardware sqrt / rsq / reciprocal, no division left in the expression
+    assert CG.to_hip(sp.sqrt(x), names, fast=True) == "nep::fsqrt((x))"
+    assert CG.to_hip(1 / sp.sqrt(x), names, fast=True) == "nep::frsq((x))"
+    assert CG.to_hip(sp.sqrt(x) / sp.sqrt(y), names, fast=True) == "(nep::fsqrt((x)) * nep::frsq((y)))"
+    assert CG.to_hip(CG._marked((x / y) ** 2), names, fast=True) == \
+        "(nep::fquot((x), (y)) * nep::fquot((x), (y)))"
+    assert CG.to_hip(1 / x, names, fast=True) == "nep::fquot(1.0f, ((x)))"
     # literals are rounded to fp32 exactly once
     assert CG.to_hip(sp.Float(0.1), names) == f"{np.float32(0.1).item().hex()}f"
     with pytest.raises(CG.TranslationError):
