@@ -251,9 +251,10 @@ def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: in
     evaluates the repair at every butterfly level) gives a row of more than 64 lanes
     MAX_UNROLL slots per lane and half the lanes, same tile: measured at fp32 16384 x 4096,
     rmsnorm_max 79.2 -> 47.2 us, stable_l2 48.8 -> 42.7 us.  `heavy_phi` (an exponential fold
-    whose producer operand is itself transcendental, softcap's tanh) splits a row that one tile
-    would cover over two tiles on half the lanes, so each lane's second loads are in flight
-    while it folds the first: softcap_lse at fp32 16384 x 4096 50.6 -> 45 us class."""
+    whose producer operand is itself transcendental, softcap's tanh) takes the same shape: twice
+    the loads in flight per lane while the transcendental work is spread over the row's lanes
+    (softcap_lse at fp32 16384 x 4096: 50.6 us at the default shape, 44.6 with the row split
+    over two tiles, 40.8 with 8 slots per lane)."""
     vec = vec_of(x2.dtype)
     vector = _is_vector(x2, ncols, vec, split_block)
     if vector and split_block and split_block < vec:
@@ -266,9 +267,7 @@ def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: in
         tpr //= 2
         unroll *= 2
     per_slot = vec if vector else 1
-    if heavy_phi and not split_block and tpr > 64 and tpr * unroll * per_slot >= ncols:
-        tpr //= 2
-    if merge_heavy and not split_block:
+    if (merge_heavy or heavy_phi) and not split_block:
         while tpr > 64 and unroll < MAX_UNROLL:
             tpr //= 2
             unroll *= 2

@@ -170,6 +170,28 @@ def test_scalar_launch_abi(recorded):
     assert T._row_last_layout(inputs[-1])[0].data_ptr() != inputs[-1].data_ptr()
 
 
+def test_launch_shapes_per_fold_class():
+    """fp32 16384 x 4096 at the default (4096, 4): the plain exponential fold keeps 4 slots on
+    256 lanes; non-exponential single-pass folds and exponential folds with a transcendental
+    producer take 8 slots on 128 lanes (one tile per row either way); two-pass folds keep the
+    whole row resident."""
+    x = torch.empty(16384, 4096)
+
+    def shape(name):
+        sk = CG.SKELETONS[name]
+        prog = T.FoldProgram(name, {}, "serial")
+        var = T._fold_variant(x, 4096, 4096, 4, resident=sk.two_pass,
+                              merge_heavy=not sk.is_log and not sk.two_pass,
+                              heavy_phi=prog.heavy_phi)
+        return var.tpr, var.unroll, var.tpr * var.unroll * 4
+
+    assert shape("logsumexp") == (256, 4, 4096)
+    assert T.FoldProgram("softcap_lse", {}, "serial").heavy_phi
+    for name in ("softcap_lse", "rmsnorm_max", "stable_l2"):
+        assert shape(name) == (128, 8, 4096), name
+    assert shape("variance")[2] >= 4096
+
+
 def test_split_launch_abi(recorded):
     x = torch.empty((2, 17), dtype=torch.bfloat16)[:, ::2]
     out = torch.empty((2,), dtype=x.dtype)
