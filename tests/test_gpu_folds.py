@@ -121,6 +121,31 @@ def test_quotient_terms_at_extreme_magnitudes(name):
                                    atol=torch.finfo(torch.float32).tiny)
 
 
+@pytest.mark.parametrize("name", ["stable_l2", "sumsq_div", "rmsnorm_max"])
+def test_repair_slopes_at_extreme_magnitudes_split(name):
+    """Repair slopes run through the hardware sqrt / rsq / reciprocal with power-of-two
+    rescaling outside [2^-64, 2^64]; the split plan evaluates them at every merge of partial
+    states.  rmsnorm_max with eps = 1e-35 (positive, as the split plan requires) at 1e-15 and
+    1e-12 puts the slope's sqrt and rsq arguments (the running mean of x^2 plus eps) below
+    2^-64 while x^2 stays a normal number."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(12)
+    cases = [(name, {"eps": 1e-35} if name == "rmsnorm_max" else {}, s)
+             for s in ((1e-15, 1e-12, 1.0, 1e15) if name == "rmsnorm_max"
+                       else (1e-39, 1e-30, 1.0, 1e18, 1e30))]
+    for skel, params, scale in cases:
+        x = ((torch.rand(6, 3000, generator=g) + 0.05) * scale).float()
+        want = R.reference(skel, x, **params)
+        for plan, block in (("serial", None), ("split", 256)):
+            _say(f"repair slopes {skel} {params} scale {scale:g} plan {plan}")
+            got = CG.run(skel, x.to(dev), plan=plan, block=block, **params).cpu()
+            ok = torch.isfinite(want)
+            assert torch.equal(torch.isfinite(got), ok), (skel, scale, plan)
+            torch.testing.assert_close(got[ok], want[ok],
+                                       rtol=R.summation_tolerance(torch.float32, 3000),
+                                       atol=torch.finfo(torch.float32).tiny)
+
+
 def test_strided_views_and_keepdim():
     dev = _dev()
     g = torch.Generator().manual_seed(3)
