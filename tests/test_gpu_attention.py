@@ -56,7 +56,8 @@ extern "C" __global__ void mfma_probe(const __bf16* a, const __bf16* b, float* c
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("shape", [(1, 2, 256, 256, 128), (2, 3, 200, 200, 128), (1, 1, 77, 77, 128),
-                                   (1, 2, 130, 333, 64), (1, 1, 1, 64, 128), (1, 4, 512, 512, 64)])
+                                   (1, 2, 130, 333, 64), (1, 1, 1, 64, 128), (1, 4, 512, 512, 64),
+                                   (1, 2, 333, 130, 128), (2, 1, 700, 65, 64)])
 def test_attention_parity(shape, causal):
     dev = _dev()
     B, H, Sq, Sk, D = shape
