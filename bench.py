@@ -215,9 +215,12 @@ def per_fold(dev, xs_dev):
     ms = graph_time(lambda i: CG.run_attention(q, k, v, causal=True), replays=3, inner=4)
     flops = 4 * 4 * 32 * 128 * 4096 * 4097 // 2
     tflops = flops / (ms * 1e-3) / 1e12
+    del q, k, v
+    gemm = gemm_ceiling_tflops(dev)
     folds["cfg5_attention_causal_bf16_4x32x4096x128"] = {
         "us": round(ms * 1e3, 1), "TFLOP_s": round(tflops, 1), "frac_mfma_bf16": round(tflops / BF16_PEAK, 4),
         "flops": flops, "query_rows_per_s": round(4 * 32 * 4096 / (ms * 1e-3), 1),
+        "bf16_gemm_TFLOP_s": round(gemm, 1), "frac_of_bf16_gemm": round(tflops / gemm, 4),
         "rocprof_pmc": attention_pmc()}
     log(f"[bench] cfg5 attention: {folds['cfg5_attention_causal_bf16_4x32x4096x128']}")
     return folds
@@ -392,6 +395,27 @@ def compile_best_table(dev):
         del module, args
         torch.cuda.empty_cache()
     return table
+
+
+def gemm_ceiling_tflops(dev, n: int = 8192, calls: int = 10) -> float:
+    """The practical bf16 MFMA rate of this GPU: torch.matmul (hipBLASLt) on contiguous
+    n x n x n bf16 operands, timed with events.  Sustained MFMA work runs below the 2.5 PFLOP/s
+    nominal (which assumes 2.4 GHz), so the attention fold is also reported against this."""
+    import torch
+
+    a = torch.randn(n, n, device=dev).bfloat16()
+    b = torch.randn(n, n, device=dev).bfloat16()
+    for _ in range(3):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(calls):
+        torch.matmul(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / calls
+    return 2 * n ** 3 / (ms * 1e-3) / 1e12
 
 
 def attention_pmc():
