@@ -14,8 +14,8 @@ import math
 import threading
 
 from neptune_codegen import hip
-from neptune_codegen.autotune import (MAX_TPR, MAX_UNROLL, UNROLL, best_config, lanes_per_row,
-                                      parameter_identity, parameter_tag, vec_of)
+from neptune_codegen.autotune import (MAX_TPR, MAX_UNROLL, UNROLL, WIDE_16BIT_ROW, best_config,
+                                      lanes_per_row, parameter_identity, parameter_tag, vec_of)
 from neptune_codegen.emitters import (BASE_OPTIONS, NO_CONTRACT, FoldVariant, RowVariant,
                                       check_supported, emit_kernel_source, emit_readout_source,
                                       emit_rms_state_source, fold_kernel_name,
@@ -254,7 +254,11 @@ def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: in
     whose producer operand is itself transcendental, softcap's tanh) takes the same shape: twice
     the loads in flight per lane while the transcendental work is spread over the row's lanes
     (softcap_lse at fp32 16384 x 4096: 50.6 us at the default shape, 44.6 with the row split
-    over two tiles, 40.8 with 8 slots per lane)."""
+    over two tiles, 40.8 with 8 slots per lane).  16-bit rows differ (bf16 sweeps at widths
+    1000-32000): `merge_heavy` folds take ~width/128 lanes (16 to 64) with 4 slots per lane (8
+    from 24576 wide) and walk several tiles -- every butterfly level costs a repair, a lane's
+    next tile only one (rmsnorm_max bf16 16384 x 4096: 31.1 -> 26.9 us); two-pass folds widen
+    lanes before slots (variance bf16 16384 x 4096: 28.5 -> 23.8 us)."""
     vec = vec_of(x2.dtype)
     vector = _is_vector(x2, ncols, vec, split_block)
     if vector and split_block and split_block < vec:
@@ -267,15 +271,24 @@ def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: in
         tpr //= 2
         unroll *= 2
     per_slot = vec if vector else 1
-    if (merge_heavy or heavy_phi) and not split_block:
+    if merge_heavy and not split_block and per_slot == 8:
+        # 16-bit rows: at most one wavefront per row, several short tiles per lane
+        tpr = min(64, max(16, 1 << max(0, (max(1, ncols // 128) - 1).bit_length())))
+        unroll = MAX_UNROLL if ncols >= WIDE_16BIT_ROW else UNROLL
+    elif (merge_heavy or heavy_phi) and not split_block:
         while tpr > 64 and unroll < MAX_UNROLL:
             tpr //= 2
             unroll *= 2
     if resident and not split_block:
+        if per_slot == 8:      # 16-bit rows: lanes first (up to 512), then slots
+            unroll = UNROLL
+            tpr = min(512, 1 << max(0, (-(-ncols // (UNROLL * per_slot)) - 1).bit_length()))
         while tpr * unroll * per_slot < ncols and unroll < MAX_UNROLL:
             unroll *= 2
         while tpr * unroll * per_slot < ncols and tpr < MAX_TPR:
             tpr *= 2
+    if per_slot == 8 and (merge_heavy or resident) and not split_block and tpr == 64:
+        waves = 1              # one row per 64-lane workgroup (bf16 8192 wide: 54.0 -> 48.7 us)
     return FoldVariant(str(x2.dtype).replace("torch.", ""), vector, tpr, unroll, waves)
 
 

@@ -191,6 +191,20 @@ def test_launch_shapes_per_fold_class():
         assert shape(name) == (128, 8, 4096), name
     assert shape("variance")[2] >= 4096
 
+    # bf16 rows at the default shape: non-exponential single-pass folds take ~width/128 lanes
+    # (16..64) and walk several tiles; two-pass folds become resident through lanes first
+    def shape16(name, ncols):
+        sk = CG.SKELETONS[name]
+        block, warps = autotune.default_config(16384, ncols, torch.bfloat16)[:2]
+        var = T._fold_variant(torch.empty(1, ncols, dtype=torch.bfloat16), ncols, block, warps,
+                              resident=sk.two_pass, merge_heavy=not sk.is_log and not sk.two_pass)
+        return var.tpr, var.unroll
+
+    assert [shape16("rmsnorm_max", n) for n in (1000, 4096, 16384, 32000)] == \
+        [(16, 4), (32, 4), (64, 4), (64, 8)]
+    assert [shape16("variance", n) for n in (1000, 4096, 16384, 32000)] == \
+        [(32, 4), (128, 4), (512, 4), (512, 8)]
+
 
 def test_split_launch_abi(recorded):
     x = torch.empty((2, 17), dtype=torch.bfloat16)[:, ::2]
