@@ -275,6 +275,12 @@ def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: in
         # 16-bit rows: at most one wavefront per row, several short tiles per lane
         tpr = min(64, max(16, 1 << max(0, (max(1, ncols // 128) - 1).bit_length())))
         unroll = MAX_UNROLL if ncols >= WIDE_16BIT_ROW else UNROLL
+    elif (merge_heavy or heavy_phi) and not split_block and per_slot == 4:
+        # fp32 rows: 8 slots per lane on the same lanes, then lanes given up while a tile would
+        # cover twice the row
+        unroll = MAX_UNROLL
+        while tpr > 16 and tpr * unroll * per_slot >= 2 * ncols:
+            tpr //= 2
     elif (merge_heavy or heavy_phi) and not split_block:
         while tpr > 64 and unroll < MAX_UNROLL:
             tpr //= 2
