@@ -244,21 +244,27 @@ def _fold_variant(x2, ncols: int, block: int, num_warps: int, *, split_block: in
                   heavy_phi: bool = False) -> FoldVariant:
     """Launch shape: 16-byte loads when the layout allows, lanes per row from BLOCK (a tile
     wider than the workgroup's lanes gives each lane up to MAX_UNROLL slots first), workgroup =
-    max(64 * num_warps, lanes per row).  `resident` (two-pass folds) widens the tile, slots
-    per lane first and then lanes, until one tile holds the whole row where that fits
-    (MAX_UNROLL slots of MAX_TPR lanes): the second pass then reads registers, not HBM.
-    `merge_heavy` (single-pass folds without the exponential fast path, whose row combine
-    evaluates the repair at every butterfly level) gives a row of more than 64 lanes
-    MAX_UNROLL slots per lane and half the lanes, same tile: measured at fp32 16384 x 4096,
-    rmsnorm_max 79.2 -> 47.2 us, stable_l2 48.8 -> 42.7 us.  `heavy_phi` (an exponential fold
-    whose producer operand is itself transcendental, softcap's tanh) takes the same shape: twice
-    the loads in flight per lane while the transcendental work is spread over the row's lanes
-    (softcap_lse at fp32 16384 x 4096: 50.6 us at the default shape, 44.6 with the row split
-    over two tiles, 40.8 with 8 slots per lane).  16-bit rows differ (bf16 sweeps at widths
-    1000-32000): `merge_heavy` folds take ~width/128 lanes (16 to 64) with 4 slots per lane (8
-    from 24576 wide) and walk several tiles -- every butterfly level costs a repair, a lane's
-    next tile only one (rmsnorm_max bf16 16384 x 4096: 31.1 -> 26.9 us); two-pass folds widen
-    lanes before slots (variance bf16 16384 x 4096: 28.5 -> 23.8 us)."""
+    max(64 * num_warps, lanes per row).  Three fold classes then adjust it (serial plan only):
+
+    * `merge_heavy` -- single-pass folds without the exponential fast path, whose row combine
+      evaluates the repair at every butterfly level -- and `heavy_phi` -- exponential folds
+      whose producer operand is itself transcendental (softcap's tanh).  fp32 rows take
+      MAX_UNROLL slots per lane on the same lanes and give lanes up while a tile would cover
+      twice the row (fp32 16384 x 4096: rmsnorm_max 79.2 -> 47.2 us, softcap_lse 50.6 -> 40.8;
+      softcap_lse 2096 x 32000: 53.8 -> 48.2).  16-bit `merge_heavy` rows take ~width/128 lanes
+      (16 to 64) with 4 slots per lane (8 from 24576 wide) and walk several tiles: a butterfly
+      level costs a repair, a lane's next tile only one (rmsnorm_max bf16 16384 x 4096: 31.1
+      -> 26.9 us).  16-bit `heavy_phi` rows of more than 64 lanes trade half the lanes for
+      twice the slots.
+    * `resident` -- two-pass folds -- widens the tile until one tile holds the whole row where
+      that fits (MAX_UNROLL slots of MAX_TPR lanes), so the second pass reads registers, not
+      HBM: fp32 widens slots first, 16-bit rows lanes first, up to 512 (variance bf16
+      16384 x 4096: 28.5 -> 23.5 us).
+    * 16-bit `merge_heavy` and `resident` rows of exactly 64 lanes run one row per 64-lane
+      workgroup (bf16 8192 wide: 54.0 -> 48.7 us).
+
+    Every default is within ~5% of a full sweep of (BLOCK, num_warps) at widths 1000-32000
+    (bf16 and fp32)."""
     vec = vec_of(x2.dtype)
     vector = _is_vector(x2, ncols, vec, split_block)
     if vector and split_block and split_block < vec:
