@@ -146,6 +146,28 @@ def test_repair_slopes_at_extreme_magnitudes_split(name):
                                        atol=torch.finfo(torch.float32).tiny)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("name", ["rmsnorm_max", "stable_l2", "variance", "softcap_lse"])
+def test_wide_rows_at_default_shapes(name, dtype):
+    """Widths 8192-32000 at the default launch shapes: 16-bit resident rows of 256-512 lanes,
+    one-wave rows with 8 slots per lane, one-row workgroups, several tiles per lane."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(13)
+    params = {"eps": 1e-6} if name == "rmsnorm_max" else {}
+    for width in (8192, 16384, 32000):
+        x = torch.randn(6, width, generator=g)
+        if name == "stable_l2":
+            x = x.abs() + 0.1
+        x = x.to(dtype)
+        _say(f"wide rows {name} {dtype} [6,{width}]")
+        got = CG.run(name, x.to(dev), **params)
+        want = R.reference(name, x, **params)
+        rtol, atol = TOL[dtype]
+        if dtype == torch.float32 and name != "softcap_lse":
+            rtol = R.summation_tolerance(dtype, width)
+        torch.testing.assert_close(got.cpu().float(), want.to(dtype).float(), rtol=rtol, atol=atol)
+
+
 def test_strided_views_and_keepdim():
     dev = _dev()
     g = torch.Generator().manual_seed(3)
