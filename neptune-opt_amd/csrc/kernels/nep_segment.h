@@ -224,10 +224,13 @@ __device__ __forceinline__ i64 block_exclusive_i64(i64 v, i64* lds) {
   return before + inc - v;
 }
 
+// Block sums of the lengths; block 0 also sets the segment kernel's status word to 1 (this
+// launch precedes the segment kernel on the same stream, so no separate fill is needed).
 template <class L>
 __device__ __forceinline__ void spans_block_sums(const L* __restrict__ lengths, i64 n,
-                                                 i64* __restrict__ sums) {
+                                                 i64* __restrict__ sums, int* __restrict__ status) {
   __shared__ i64 lds[kSpanThreads / 64];
+  if (status != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *status = 1;
   const i64 base = (i64)blockIdx.x * kSpanBlock + (i64)threadIdx.x * kSpanPer;
   i64 s = 0;
 #pragma unroll

@@ -494,8 +494,8 @@ def emit_segment_spans_source() -> str:
     for tag, ctype in (("i32", "int"), ("i64", "long long")):
         parts.append(
             f'extern "C" __global__ void __launch_bounds__(256) segment_spans_sums_{tag}('
-            "const void* lengths, long long n, long long* sums) {\n"
-            f"  nep::spans_block_sums<{ctype}>((const {ctype}*)lengths, n, sums);\n}}\n")
+            "const void* lengths, long long n, long long* sums, int* status) {\n"
+            f"  nep::spans_block_sums<{ctype}>((const {ctype}*)lengths, n, sums, status);\n}}\n")
         parts.append(
             f'extern "C" __global__ void __launch_bounds__(256) segment_spans_scan_{tag}('
             "const void* lengths, long long n, const long long* sums, long long* spans) {\n"

@@ -400,17 +400,18 @@ def _spans_program() -> hip.Program:
         return _SPANS_PROGRAM
 
 
-def _device_spans(data, segments, *, offsets):
+def _device_spans(data, segments, *, offsets, status=None):
     """[start, end) boundaries for the fused-validation launch: offsets as given, lengths as an
     int64 prefix sum (the same values `_segment_spans` builds) by two HIP launches -- block
     sums, then a per-block scan on top of the preceding blocks; no asserts here (the segment
-    kernel checks the spans)."""
+    kernel checks the spans).  With lengths, the first launch also sets `status` (one int32)
+    to 1; returns (spans, status set)."""
     import torch
 
     from neptune_codegen.emitters import SPAN_BLOCK
 
     if offsets:
-        return segments
+        return segments, False
     lengths = segments.contiguous()
     n = lengths.shape[0]
     spans = torch.empty(n + 1, dtype=torch.int64, device=segments.device)
@@ -420,12 +421,14 @@ def _device_spans(data, segments, *, offsets):
     device = segments.device.index if segments.device.index is not None else torch.cuda.current_device()
     prog = _spans_program()
     stream = hip.current_stream(segments.device)
-    prog.kernel(f"segment_spans_sums_{tag}", (hip.PTR, hip.I64, hip.PTR), 256, device).launch(
-        (nblocks,), (lengths.data_ptr(), n, sums.data_ptr()), stream)
+    prog.kernel(f"segment_spans_sums_{tag}", (hip.PTR, hip.I64, hip.PTR, hip.PTR), 256,
+                device).launch((nblocks,), (lengths.data_ptr(), n, sums.data_ptr(),
+                                            status.data_ptr() if status is not None else 0),
+                               stream)
     prog.kernel(f"segment_spans_scan_{tag}", (hip.PTR, hip.I64, hip.PTR, hip.PTR), 256,
                 device).launch((nblocks,), (lengths.data_ptr(), n, sums.data_ptr(),
                                             spans.data_ptr()), stream)
-    return spans
+    return spans, status is not None
 
 
 def _launch_segment(name, data, segments, params, plan, *, wrapper=None):
@@ -443,8 +446,10 @@ def _launch_segment(name, data, segments, params, plan, *, wrapper=None):
     out = torch.empty(shape, dtype=data.dtype, device=data.device)
     nseg = shape[0]
     if type(nseg) is int and nseg > 0 and type(channels) is int and channels > 0:
-        spans = _device_spans(data, segments, offsets=params["offsets"])
-        status = torch.ones(1, dtype=torch.int32, device=data.device)
+        status = torch.empty(1, dtype=torch.int32, device=data.device)
+        spans, status_set = _device_spans(data, segments, offsets=params["offsets"], status=status)
+        if not status_set:
+            status.fill_(1)
         cover = -1 if params["offsets"] or params["unsafe"] else data.shape[0]
         flat = data.reshape(data.shape[0], channels)
         launch_segment_kernel(compile_segment_reduction(name, params, plan), flat, spans, out,

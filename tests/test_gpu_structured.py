@@ -223,10 +223,13 @@ def test_segment_fused_descriptor_check_matches_reference_asserts():
                 reference_ok = False
             _say(f"fused descriptor check {indices} offsets={is_offsets} unsafe={unsafe} {idx_dtype}")
             seg_dev = seg.to(dev)
-            spans = TO._device_spans(data, seg_dev, offsets=is_offsets)
+            status = torch.zeros(1, dtype=torch.int32, device=dev)
+            spans, status_set = TO._device_spans(data, seg_dev, offsets=is_offsets, status=status)
+            assert status_set == (not is_offsets)
+            if not status_set:
+                status.fill_(1)
             nseg = spans.shape[0] - 1
             out = torch.empty(nseg, 16, dtype=torch.float16, device=dev)
-            status = torch.ones(1, dtype=torch.int32, device=dev)
             cover = -1 if is_offsets or unsafe else data.shape[0]
             TO.launch_segment_kernel(program_off if is_offsets else program, data.to(dev), spans, out,
                                      status=status, cover=cover)
@@ -250,6 +253,8 @@ def test_lengths_prefix_sum_kernel_is_exact(dtype):
         if dtype == torch.int64:
             lengths[n // 2] = 1 << 40
         print(f"spans scan {dtype} n={n}", flush=True)
-        got = _device_spans(None, lengths.to(dev), offsets=False).cpu()
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
+        got, status_set = _device_spans(None, lengths.to(dev), offsets=False, status=status)
         want = torch.cat([torch.zeros(1, dtype=torch.int64), lengths.to(torch.int64).cumsum(0)])
-        assert got.dtype == torch.int64 and torch.equal(got, want)
+        assert got.dtype == torch.int64 and torch.equal(got.cpu(), want)
+        assert status_set and status.item() == 1, "the first spans launch sets the status word"
