@@ -120,14 +120,24 @@ def measure_fold(name, make, nbytes, rows, launches=20):
     return out
 
 
-def per_fold(dev, xs_dev):
+def per_fold(dev, xs_cpu, xs_dev, cpu: bool = True):
+    """GPU time of every configuration (cold cache), and beside each, when `cpu` is set, the
+    oracle's eager CPU form timed on a bounded sample of the same seeded input."""
     import torch
 
     import neptune_codegen as CG
+    from oracle import references as R
 
     folds = {}
+    host = CpuHost() if cpu else None
+
+    def beside(key, label, fn, units, unit, sample):
+        if host is not None:
+            folds[key]["cpu"] = host.time(label, fn, units, unit, sample)
+
     # cfg1: fp32 logsumexp [8192, 1024], N(0, 3^2), seed 0
-    x1 = (3 * torch.randn(8192, 1024, generator=seeded(0))).to(dev)
+    x1c = 3 * torch.randn(8192, 1024, generator=seeded(0))
+    x1 = x1c.to(dev)
     b1 = 8192 * 1024 * 4 + 8192 * 4
 
     def make1(n):
@@ -135,8 +145,11 @@ def per_fold(dev, xs_dev):
         return [lambda x=x: CG.run("logsumexp", x) for x in xs]
 
     folds["cfg1_logsumexp_f32_8192x1024"] = measure_fold("cfg1", make1, b1, 8192)
+    beside("cfg1_logsumexp_f32_8192x1024", "cfg1", lambda: R.reference("logsumexp", x1c), b1 / 1e9,
+           "GB/s", "the whole [8192, 1024] input; torch.logsumexp(x.float(), -1)")
     # every registered scalar skeleton (serial plan) at one HBM-scale shape: fp32 [16384, 4096]
-    xl = torch.randn(16384, 4096, generator=seeded(12)).to(dev)
+    xlc = torch.randn(16384, 4096, generator=seeded(12))
+    xl = xlc.to(dev)
     bl = 16384 * 4096 * 4 + 16384 * 4
     for name in sorted(CG.supported()):
         params = {"eps": 1e-6} if name == "rmsnorm_max" else {}
@@ -145,8 +158,11 @@ def per_fold(dev, xs_dev):
             xs = [xl] + [xl.clone() for _ in range(n - 1)]
             return [lambda y=y: CG.run(name, y, **params) for y in xs]
 
-        folds[f"skeleton_{name}_f32_16384x4096"] = measure_fold(f"skeleton {name}", makel, bl, 16384)
-    del xl
+        key = f"skeleton_{name}_f32_16384x4096"
+        folds[key] = measure_fold(f"skeleton {name}", makel, bl, 16384)
+        beside(key, f"skeleton {name}", lambda name=name, params=params: R.reference(name, xlc[:2048], **params),
+               bl / 8 / 1e9, "GB/s", f"rows 0-2047 of the input (1/8); oracle reference('{name}')")
+    del xl, xlc
     for w in (128, 1000, 4096, 32000, "split"):
         x = xs_dev[w]
 
@@ -158,6 +174,11 @@ def per_fold(dev, xs_dev):
         rows = 64 if w == "split" else 16384
         key = "cfg2_split_bf16_64x262144" if w == "split" else f"cfg2_logsumexp_bf16_16384x{w}"
         folds[key] = measure_fold(key, make, cfg2_bytes(w), rows)
+        part = 16 if w == "split" else (16384 if w <= 1000 else 2048)
+        xc = xs_cpu[w][:part]
+        beside(key, key, lambda xc=xc: R.reference("logsumexp", xc).bfloat16(),
+               cfg2_bytes(w) * part / rows / 1e9, "GB/s",
+               f"rows 0-{part - 1} of {rows}; torch.logsumexp(x.float(), -1).to(bf16)")
     # log_softmax readout of the cfg2 W=32000 rows: the fold plus a full-row write
     x = xs_dev[32000]
 
@@ -165,12 +186,18 @@ def per_fold(dev, xs_dev):
         xs = [x] + [x.clone() for _ in range(n - 1)]
         return [lambda y=y: CG.run_log_softmax(y) for y in xs]
 
+    b_ls = 2 * 16384 * 32000 * 2
     folds["cfg2_log_softmax_bf16_16384x32000"] = measure_fold(
-        "cfg2 log_softmax W=32000", make_ls, 2 * 16384 * 32000 * 2, 16384)
+        "cfg2 log_softmax W=32000", make_ls, b_ls, 16384)
+    xc = xs_cpu[32000][:1024]
+    beside("cfg2_log_softmax_bf16_16384x32000", "log_softmax",
+           lambda: torch.log_softmax(xc.float(), -1).bfloat16(), b_ls / 16 / 1e9, "GB/s",
+           "rows 0-1023 of 16384; torch.log_softmax(x.float(), -1).to(bf16)")
     # cfg3: RMSNorm and L2-normalize bf16 [32768, 4096], seed 3
     g3 = seeded(3)
-    x3 = torch.randn(32768, 4096, generator=g3).bfloat16().to(dev)
-    gamma = (1 + 0.1 * torch.randn(4096, generator=g3)).bfloat16().to(dev)
+    x3c = torch.randn(32768, 4096, generator=g3).bfloat16()
+    gammac = (1 + 0.1 * torch.randn(4096, generator=g3)).bfloat16()
+    x3, gamma = x3c.to(dev), gammac.to(dev)
     b3 = 2 * 32768 * 4096 * 2 + 4096 * 2
 
     def make3(n, l2=False):
@@ -181,17 +208,26 @@ def per_fold(dev, xs_dev):
 
     folds["cfg3_rms_norm_bf16_32768x4096"] = measure_fold("cfg3 rms", make3, b3, 32768)
     folds["cfg3_l2_normalize_bf16_32768x4096"] = measure_fold("cfg3 l2", lambda n: make3(n, True), b3 - 8192, 32768)
-    del x3
+    x3s = x3c[:4096]
+    beside("cfg3_rms_norm_bf16_32768x4096", "cfg3 rms", lambda: R.rms_norm_reference(x3s, gammac, 1e-6),
+           (2 * 4096 * 4096 * 2 + 4096 * 2) / 1e9, "GB/s",
+           "rows 0-4095 of 32768; v = x.float(); (v * rsqrt(mean(v*v) + eps)).to(bf16) * gamma")
+    beside("cfg3_l2_normalize_bf16_32768x4096", "cfg3 l2", lambda: R.l2_normalize_reference(x3s, 1e-6),
+           2 * 4096 * 4096 * 2 / 1e9, "GB/s", "rows 0-4095 of 32768; F.normalize(x.float(), dim=-1, eps=1e-6).to(bf16)")
+    del x3, x3c
     # cfg4: fp16 CSR segment sum / mean, 65536 segments, Poisson(20) lengths in [0, 200]
     g4 = seeded(4)
     lengths = torch.poisson(torch.full((65536,), 20.0), generator=g4).clamp(0, 200).to(torch.int32)
     total = int(lengths.sum())
-    data = torch.randn(total, 128, generator=g4).half().to(dev)
-    offsets = torch.cat([torch.zeros(1, dtype=torch.int32), lengths.cumsum(0).to(torch.int32)]).to(dev)
+    datac = torch.randn(total, 128, generator=g4).half()
+    offsetsc = torch.cat([torch.zeros(1, dtype=torch.int32), lengths.cumsum(0).to(torch.int32)])
+    data, offsets = datac.to(dev), offsetsc.to(dev)
     b4 = 256 * total + 4 * 65537 + 256 * 65536
     from neptune_codegen.torch_op import compile_segment_reduction, launch_segment_kernel
 
     out4 = torch.empty(65536, 128, dtype=torch.float16, device=dev)
+    nseg_cpu = 8192
+    tok_cpu = int(offsetsc[nseg_cpu])
     for reduce in ("sum", "mean"):
         program = compile_segment_reduction(f"segment_{reduce}", {"offsets": True})
 
@@ -206,24 +242,80 @@ def per_fold(dev, xs_dev):
         key = f"cfg4_segment_{reduce}_f16_65536x128"
         folds[key] = measure_fold(f"cfg4 {reduce} kernel", make4, b4, 65536)
         folds[key]["op_us_with_descriptor_asserts"] = measure_fold(f"cfg4 {reduce} op", make4_op, b4, 65536)["us"]
+        ds, os_ = datac[:tok_cpu], offsetsc[:nseg_cpu + 1]
+        beside(key, f"cfg4 {reduce}", lambda reduce=reduce, ds=ds, os_=os_:
+               R.segment_reference(ds, os_, reduce, offsets=True),
+               (256 * tok_cpu + 4 * (nseg_cpu + 1) + 256 * nseg_cpu) / 1e9, "GB/s",
+               f"segments 0-{nseg_cpu - 1} of 65536 ({tok_cpu} tokens); "
+               f"torch.segment_reduce(data, '{reduce}', offsets=..., axis=0)")
     folds["cfg4_segment_tokens"] = total
-    del data
+    del data, datac
     # cfg5: causal attention fold, B=4 H=32 S=4096 D=128 bf16, seed 5
     g5 = seeded(5)
     shape = (4, 32, 4096, 128)
-    q, k, v = ((torch.randn(*shape, generator=g5).bfloat16()).to(dev) for _ in range(3))
+    qkv = [torch.randn(*shape, generator=g5).bfloat16() for _ in range(3)]
+    q, k, v = (t.to(dev) for t in qkv)
     ms = graph_time(lambda i: CG.run_attention(q, k, v, causal=True), replays=3, inner=4)
     flops = 4 * 4 * 32 * 128 * 4096 * 4097 // 2
     tflops = flops / (ms * 1e-3) / 1e12
     del q, k, v
     gemm = gemm_ceiling_tflops(dev)
-    folds["cfg5_attention_causal_bf16_4x32x4096x128"] = {
+    key5 = "cfg5_attention_causal_bf16_4x32x4096x128"
+    folds[key5] = {
         "us": round(ms * 1e3, 1), "TFLOP_s": round(tflops, 1), "frac_mfma_bf16": round(tflops / BF16_PEAK, 4),
         "flops": flops, "query_rows_per_s": round(4 * 32 * 4096 / (ms * 1e-3), 1),
         "bf16_gemm_TFLOP_s": round(gemm, 1), "frac_of_bf16_gemm": round(tflops / gemm, 4),
         "rocprof_pmc": attention_pmc()}
-    log(f"[bench] cfg5 attention: {folds['cfg5_attention_causal_bf16_4x32x4096x128']}")
+    log(f"[bench] cfg5 attention: {folds[key5]}")
+    qh, kh, vh = (t[0:1, 0:2] for t in qkv)
+    beside(key5, "cfg5 attention", lambda: R.attention_reference(qh, kh, vh, causal=True),
+           flops / 64 / 1e12, "TFLOP/s",
+           "heads (0,0) and (0,1) of 128, i.e. 1/64 of the FLOPs, scaled linearly to the whole "
+           "job; fp32 softmax(scale*QK^T + causal) V (SDPA math form)")
     return folds
+
+
+class CpuHost:
+    """Times the oracle's eager CPU forms on the host cores.
+
+    Threads: the process's CPU share (OMP_NUM_THREADS when set, else the affinity mask).  The
+    GPU box gives one GPU's job 16 cores and sets OMP_NUM_THREADS=16; os.cpu_count() counts the
+    whole host, whose other cores belong to other jobs, so it is recorded but not used."""
+
+    def __init__(self):
+        import torch
+
+        env = os.environ.get("OMP_NUM_THREADS", "")
+        self.threads = int(env) if env.isdigit() and int(env) > 0 else len(os.sched_getaffinity(0))
+        torch.set_num_threads(self.threads)
+        self.model = cpu_model()
+        self.host_cpus = os.cpu_count()
+
+    def time(self, label, fn, units, unit, sample, seconds: float = 1.0):
+        """Median wall time of fn() over repeats filling about `seconds` (after one warm-up),
+        reported as units / time."""
+        fn()
+        times, t_end = [], time.perf_counter() + seconds
+        while time.perf_counter() < t_end or len(times) < 3:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        med = sorted(times)[len(times) // 2]
+        out = {"value": round(units / med, 3), "unit": unit, "cores": self.threads,
+               "host_cpus": self.host_cpus, "model": self.model, "kind": "port",
+               "median_s": round(med, 5), "runs": len(times), "sample": sample}
+        log(f"[bench] cpu {label}: {out['value']} {unit} ({med * 1e3:.2f} ms per sample)")
+        return out
+
+
+def cpu_model() -> str:
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(xs_cpu, seconds_target: float = 15.0):
@@ -233,7 +325,7 @@ def cpu_baseline(xs_cpu, seconds_target: float = 15.0):
 
     from oracle import references as R
 
-    threads = torch.get_num_threads()
+    host = CpuHost()
     frac = 1 / 4
     total_bytes, total_s = 0.0, 0.0
     deadline = time.perf_counter() + seconds_target
@@ -243,17 +335,19 @@ def cpu_baseline(xs_cpu, seconds_target: float = 15.0):
             rows = max(1, int(x.shape[0] * frac))
             sample = x[:rows]
             t0 = time.perf_counter()
-            R.reference("logsumexp", sample)
+            R.reference("logsumexp", sample).to(torch.bfloat16)
             total_s += time.perf_counter() - t0
             total_bytes += cfg2_bytes(w) * rows / x.shape[0]
         reps += 1
         if time.perf_counter() > deadline:
             break
     gbs = total_bytes / total_s / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": host.threads, "host_cpus": host.host_cpus,
+            "model": host.model, "kind": "port",
             "sample": f"1/4 of the rows of each cfg2 input (widths 128/1000/4096/32000 and the "
                       f"64x262144 split input), {reps} passes, {total_s:.1f} s of CPU work; "
-                      "oracle.references.reference('logsumexp') = torch.logsumexp(x.float(), -1)"}
+                      "oracle.references.reference('logsumexp') = torch.logsumexp(x.float(), -1), "
+                      "rounded to bf16"}
 
 
 def pmc_traffic():
@@ -548,7 +642,7 @@ def main():
                 "kernel": "logsumexp_serial_bf16 (16384 x 32000)", "kernel_us": round(dom_ms * 1e3, 2),
                 "bytes_per_launch": dom_bytes}
     log(f"[bench] dominant kernel {dom_ms * 1e3:.1f} us, {achieved:.1f} GB/s")
-    folds = None if args.no_folds else per_fold(dev, xs)
+    folds = None if args.no_folds else per_fold(dev, xs_cpu, xs, cpu=not args.no_cpu)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(xs_cpu)

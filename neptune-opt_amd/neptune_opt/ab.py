@@ -13,8 +13,10 @@ neptune_opt and call the op's handle (e.g. `neptune_codegen.op_handle`) or run `
 """
 from __future__ import annotations
 
+import contextlib
 import copy
 import dataclasses
+import itertools
 import math
 import os
 import statistics
@@ -40,23 +42,48 @@ class FatalCudaError(RuntimeError):
     """The device context is unusable; stop the process rather than fall back in it."""
 
 
-def _raise_if_fatal_cuda(error):
-    """Raise FatalCudaError when `error` or anything in its cause/context chain reports a
-    context-destroying device failure; otherwise return (touching no GPU state)."""
-    pending, seen = [error], set()
+def _causes(error):
+    """error, then everything reachable through __cause__ / __context__, each once."""
+    seen, pending = set(), [error]
     while pending:
         current = pending.pop()
-        if current is None or id(current) in seen:
-            continue
-        seen.add(id(current))
+        if current is not None and id(current) not in seen:
+            seen.add(id(current))
+            yield current
+            pending += [current.__cause__, current.__context__]
+
+
+def fatal_cause(error):
+    """The exception in error's chain that reports a lost device context, or None."""
+    for current in _causes(error):
         if isinstance(current, FatalCudaError):
-            raise current
+            return current
         text = str(current).lower()
         if any(token in text for token in _FATAL_TOKENS):
-            raise FatalCudaError(
-                "GPU context failure: stop this process; baseline files may exist but "
-                "in-process execution/fallback is unsafe. Original error: " + str(current)) from error
-        pending.extend((current.__cause__, current.__context__))
+            return current
+    return None
+
+
+def _raise_if_fatal_cuda(error):
+    """Raise FatalCudaError when error's chain reports a lost device context; otherwise return.
+    Only the message text is inspected: the GPU is not touched."""
+    cause = fatal_cause(error)
+    if isinstance(cause, FatalCudaError):
+        raise cause
+    if cause is not None:
+        raise FatalCudaError("GPU context failure: stop this process; baseline files may exist "
+                             "but in-process execution/fallback is unsafe. Original error: "
+                             + str(cause)) from error
+
+
+@contextlib.contextmanager
+def _fatal_errors_escalate():
+    """Let exceptions of the body propagate, as FatalCudaError when the device context is lost."""
+    try:
+        yield
+    except Exception as error:  # noqa: BLE001
+        _raise_if_fatal_cuda(error)
+        raise
 
 
 @dataclasses.dataclass
@@ -106,79 +133,103 @@ def choose_faster(baseline_ms: float, fused_ms: float, margin: float = MARGIN) -
                             "unmodified baseline was kept")
 
 
-def _bounded_names(items, allowed, what):
-    """Distinct names from `allowed`, reading at most len(allowed)+1 items of any iterable."""
+def _name_messages(what, allowed):
+    names = "/".join(allowed)
+    return {"not_iterable": f"{what} must be a finite iterable of {names} names",
+            "string": f"{what} must be a finite iterable of {names} names",
+            "bad_item": f"{what} must contain distinct {names} names",
+            "too_many": f"{what} must contain at most {len(allowed)} distinct names"}
+
+
+def _bounded_names(items, allowed, messages):
+    """The distinct names of `items`, each one of `allowed`, as a tuple.  At most
+    len(allowed) + 1 items are read, so an endless iterable is refused, not exhausted.
+    `messages` maps not_iterable / string / bad_item / too_many to the ValueError texts."""
     if isinstance(items, (str, bytes)):
-        raise ValueError(f"{what} must be a finite iterable of {'/'.join(allowed)} names")
+        raise ValueError(messages["string"])
     try:
         iterator = iter(items)
     except TypeError as error:
-        raise ValueError(f"{what} must be a finite iterable of {'/'.join(allowed)} names") from error
+        raise ValueError(messages["not_iterable"]) from error
     names = []
-    for _ in range(len(allowed) + 1):
-        try:
-            name = next(iterator)
-        except StopIteration:
-            return tuple(names)
+    for name in itertools.islice(iterator, len(allowed) + 1):
         if not isinstance(name, str) or name not in allowed or name in names:
-            raise ValueError(f"{what} must contain distinct {'/'.join(allowed)} names")
+            raise ValueError(messages["bad_item"])
         names.append(name)
-    raise ValueError(f"{what} must contain at most {len(allowed)} distinct names")
+    if len(names) > len(allowed):
+        raise ValueError(messages["too_many"])
+    return tuple(names)
 
 
 # ---------------------------------------------------------------- steps (injectable for tests)
+def _storage_shared(base, other) -> bool:
+    """True when the two programs share their graph module or any state tensor's storage."""
+    import torch
+
+    if other is base or other.graph_module is base.graph_module:
+        return True
+    for name, tensor in base.state_dict.items():
+        twin = other.state_dict[name]
+        if twin is tensor:
+            return True
+        if isinstance(tensor, torch.Tensor) and tensor.numel() and tensor.data_ptr() == twin.data_ptr():
+            return True
+    return False
+
+
+def _independent_copy(ep_base, module, args, export_kwargs):
+    """A program equal to ep_base that shares no graph and no weights with it: a deep copy,
+    or, where this torch cannot deep-copy an ExportedProgram faithfully, a fresh export of a
+    deep copy of the module (an export of `module` itself would share its parameters)."""
+    import torch
+
+    try:
+        copied = copy.deepcopy(ep_base)
+        if not _storage_shared(ep_base, copied):
+            return copied
+    except Exception as error:  # noqa: BLE001
+        _raise_if_fatal_cuda(error)
+    return torch.export.export(copy.deepcopy(module), tuple(args), **export_kwargs)
+
+
 def _export_pair(module, args, export_kwargs, plan=None, *, baseline=None, capabilities=(),
                  verification_inputs=None, rtol=1e-3, atol=1e-4, max_ulps=None):
-    """(baseline EP, candidate EP or None, report).  The candidate is a deep copy (or a fresh
-    export of a copied module) that shares no weights with the baseline."""
+    """(baseline program, fused candidate or None, apply's report).  The baseline is exported
+    untouched (its errors propagate); the candidate is an independent copy rewritten by a
+    verified `apply`.  Any candidate failure becomes a report, never an exception."""
     import torch
 
     import neptune_opt
 
-    try:
+    with _fatal_errors_escalate():
         ep_base = baseline if baseline is not None else torch.export.export(
             module, tuple(args), **export_kwargs)
-    except Exception as error:  # noqa: BLE001 -- a baseline export error is the caller's
-        _raise_if_fatal_cuda(error)
-        raise
+    options = {"rtol": rtol, "atol": atol, "max_ulps": max_ulps}
+    if plan is not None:
+        options["plan"] = plan
+    if capabilities:
+        options["capabilities"] = capabilities
+    if verification_inputs is not None:
+        options["verification_inputs"] = verification_inputs
     try:
-        try:
-            ep_fused = copy.deepcopy(ep_base)
-            if ep_fused is ep_base or ep_fused.graph_module is ep_base.graph_module:
-                raise RuntimeError("candidate copy shares the baseline graph")
-            for name, value in ep_base.state_dict.items():
-                other = ep_fused.state_dict[name]
-                if value is other or (isinstance(value, torch.Tensor) and value.numel()
-                                      and value.data_ptr() == other.data_ptr()):
-                    raise RuntimeError("candidate copy shares baseline weights")
-        except Exception as error:  # noqa: BLE001 -- deepcopy support varies across torch versions
-            _raise_if_fatal_cuda(error)
-            ep_fused = torch.export.export(copy.deepcopy(module), tuple(args), **export_kwargs)
-        kwargs = {"rtol": rtol, "atol": atol, "max_ulps": max_ulps}
-        if plan is not None:
-            kwargs["plan"] = plan
-        if capabilities:
-            kwargs["capabilities"] = capabilities
-        if verification_inputs is not None:
-            kwargs["verification_inputs"] = verification_inputs
-        report = neptune_opt.apply(ep_fused, verify_with=(module, tuple(args)), **kwargs)
+        candidate = _independent_copy(ep_base, module, args, export_kwargs)
+        report = neptune_opt.apply(candidate, verify_with=(module, tuple(args)), **options)
     except Exception as error:  # noqa: BLE001 -- the optional candidate never breaks the baseline
         _raise_if_fatal_cuda(error)
-        ep_fused = None
-        report = neptune_opt.Report(skipped=[("candidate-failed", f"{type(error).__name__}: {error}")])
-    return ep_base, ep_fused, report
+        return ep_base, None, neptune_opt.Report(
+            skipped=[("candidate-failed", f"{type(error).__name__}: {error}")])
+    return ep_base, candidate, report
 
 
 def _package(ep, directory: str, name: str) -> str:
+    """AOTI-compile ep into <directory>/<name>.pt2.  The fused HIP ops are dispatcher calls
+    (AOTI's proxy executor reaches their C++ kernels), so no user-kernel options apply."""
     import torch
 
-    path = os.path.join(directory, f"{name}.pt2")
-    try:
-        torch._inductor.aoti_compile_and_package(ep, package_path=path)
-    except Exception as error:  # noqa: BLE001
-        _raise_if_fatal_cuda(error)
-        raise
-    return path
+    target = os.path.join(directory, name + ".pt2")
+    with _fatal_errors_escalate():
+        torch._inductor.aoti_compile_and_package(ep, package_path=target)
+    return target
 
 
 def _load(path: str):
@@ -187,46 +238,51 @@ def _load(path: str):
     return torch._inductor.aoti_load_package(path)
 
 
+def _package_output_problem(index, x, y, tol):
+    """Why package outputs x and y (leaf `index`) disagree, or None: both must be tensors of
+    equal metadata, floating values all finite and within tol, others equal."""
+    import torch
+
+    from neptune_opt.verification import _value_difference
+
+    if not (isinstance(x, torch.Tensor) and isinstance(y, torch.Tensor)):
+        return f"output {index} is not a tensor"
+    if (x.shape, x.dtype, x.device) != (y.shape, y.dtype, y.device):
+        return f"output {index} shape/dtype/device differs"
+    if not (x.is_floating_point() or x.is_complex()):
+        return None if torch.equal(x, y) else f"output {index} integer/bool values differ"
+    if not bool(torch.isfinite(x).all()) or not bool(torch.isfinite(y).all()):
+        return f"output {index} contains nonfinite values"
+    return _value_difference(index, x, y, tol)
+
+
 def _same_numbers(fa, fb, args, *, rtol: float = 1e-3, atol: float = 1e-4,
                   max_ulps: int | None = None) -> tuple:
-    """(ok, detail): both callables give tensor-only, all-finite outputs that agree within
-    tolerance (integers exactly; fp16/bf16 optionally within max_ulps)."""
+    """(ok, detail): fa(*args) and fb(*args) give the same pytree of finite tensors, equal
+    within (rtol, atol) -- integers exactly, fp16/bf16 optionally within max_ulps ULPs.  Any
+    execution error refuses; a lost device context raises."""
     import torch
     from torch.utils._pytree import tree_flatten
+
+    from neptune_opt.verification import Tolerance
 
     _validate_nonnegative("rtol", rtol)
     _validate_nonnegative("atol", atol)
     if max_ulps is not None and (type(max_ulps) is not int or max_ulps < 0):
         raise ValueError("max_ulps must be a nonnegative integer or None")
+    tol = Tolerance(rtol, atol, max_ulps)
     try:
         with torch.no_grad():
-            a, spec_a = tree_flatten(fa(*args))
-            b, spec_b = tree_flatten(fb(*args))
-        if spec_a != spec_b:
+            left, left_spec = tree_flatten(fa(*args))
+            right, right_spec = tree_flatten(fb(*args))
+        if left_spec != right_spec:
             return False, "output pytree structure differs"
-        for i, (x, y) in enumerate(zip(a, b)):
-            if not isinstance(x, torch.Tensor) or not isinstance(y, torch.Tensor):
-                return False, f"output {i} is not a tensor"
-            if x.shape != y.shape or x.dtype != y.dtype or x.device != y.device:
-                return False, f"output {i} shape/dtype/device differs"
-            if not (x.is_floating_point() or x.is_complex()):
-                if not torch.equal(x, y):
-                    return False, f"output {i} integer/bool values differ"
-                continue
-            if not (torch.isfinite(x).all().item() and torch.isfinite(y).all().item()):
-                return False, f"output {i} contains nonfinite values"
-            if max_ulps is None:
-                torch.testing.assert_close(x, y, rtol=rtol, atol=atol, equal_nan=False)
-            else:
-                from neptune_opt import _compare_trees
-
-                ok, detail = _compare_trees(x, y, rtol=rtol, atol=atol, max_ulps=max_ulps)
-                if not ok:
-                    return False, f"output {i}: {detail}"
-    except Exception as error:  # noqa: BLE001 -- any execution/comparison failure refuses
+        problems = (_package_output_problem(i, x, y, tol) for i, (x, y) in enumerate(zip(left, right)))
+        problem = next((p for p in problems if p), None)
+    except Exception as error:  # noqa: BLE001 -- any execution or comparison failure refuses
         _raise_if_fatal_cuda(error)
         return False, f"{type(error).__name__}: {error}"
-    return True, ""
+    return (False, problem) if problem else (True, "")
 
 
 def _ab_time(fa, fb, args, reps: int = 20, rounds: int = 5, warmup: int = 3) -> tuple:
@@ -392,7 +448,8 @@ def compile_best(module, args, *, package_dir: str | None = None, margin: float 
     segment_pool every case must avoid a regression above `regression_margin`."""
     import torch
 
-    capabilities = _bounded_names(capabilities, ("rms_norm", "segment_pool"), "capabilities")
+    capabilities = _bounded_names(capabilities, ("rms_norm", "segment_pool"),
+                                  _name_messages("capabilities", ("rms_norm", "segment_pool")))
     if max_ulps is not None and (type(max_ulps) is not int or max_ulps < 0):
         raise ValueError("max_ulps must be a nonnegative integer or None")
     for name, value in (("margin", margin), ("regression_margin", regression_margin),
@@ -401,7 +458,7 @@ def compile_best(module, args, *, package_dir: str | None = None, margin: float 
     for name, value in (("reps", reps), ("rounds", rounds)):
         if isinstance(value, bool) or not isinstance(value, int) or value < 1:
             raise ValueError(f"{name} must be a positive integer")
-    plans = _bounded_names(plans, ("serial", "split"), "plans")
+    plans = _bounded_names(plans, ("serial", "split"), _name_messages("plans", ("serial", "split")))
     if not plans:
         raise ValueError("plans must not be empty")
     args = tuple(args)

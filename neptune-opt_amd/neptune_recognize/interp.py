@@ -146,14 +146,10 @@ def _as_expr(arg, env):
 
 
 def _flatten_nodes(arg, out: list) -> None:
-    if hasattr(arg, "op"):
-        out.append(arg)
-    elif isinstance(arg, (tuple, list)):
-        for item in arg:
-            _flatten_nodes(item, out)
-    elif isinstance(arg, dict):
-        for item in arg.values():
-            _flatten_nodes(item, out)
+    """Append to `out` the graph nodes inside a (possibly nested) FX argument, in order."""
+    import torch.fx
+
+    torch.fx.node.map_arg(arg, out.append)
 
 
 def _operand(node, env, index=0) -> sp.Expr:

@@ -1,39 +1,83 @@
 """Targeted lowering of compound ATen ops into the decomposed form recognition reads.
 
-`aten.logsumexp` and (opt-in) `aten.log_softmax` / `aten._log_softmax` over the last dimension
-are expanded into explicit fp32 steps: an optional cast to fp32, the amax with torch's infinity
-guard, exp/sum/log and the add that ends the LSE region; log_softmax adds the readout
-x - LSE with NaN on rows whose LSE is +inf (torch's row classification), and the final cast.
-Nothing else is decomposed.  The step list, the node metadata mark `neptune_lowering` and the
-transactional commit follow the reference (neptune_recognize/lowering.py:1-282), because
-apply() pairs each lowered node with the region recognised from it.
+Only `aten.logsumexp` and (opt-in, through neptune_opt) `aten.log_softmax` /
+`aten._log_softmax` over the last dimension are expanded; nothing else is decomposed.  The
+expansion is the reference's step list (neptune_recognize/lowering.py:64-111), because the
+recognised region and the rewrite's readout fusion read exactly those nodes:
+
+    [x = x.to(fp32)]                                     16-bit inputs accumulate in fp32
+    m = amax(x, dim, keepdim)
+    m_safe = where(|m| == inf, 0, m)                     torch.logsumexp's infinity guard
+    lse = m_safe + log(sum(exp(x - m_safe), dim, keepdim))
+    log_softmax:  where(lse == inf, nan, x - lse)        torch's NaN rows for +inf inputs
+    logsumexp without keepdim: squeeze(lse, dim)
+    [out = result.to(output dtype)]
+
+Every emitted node carries `meta["neptune_lowering"] = <compound node name>`, so that a caller
+can find the region grown from one compound node.  The table is data: one interpreter runs it
+on Fake/meta tensors (the metadata of every step, computed by torch) and the same interpreter
+emits it as graph nodes.  The structural gate certifies a complete fp32 LSE region, not
+bitwise equality with torch's fused kernels.
 """
 from __future__ import annotations
 
 import copy
+import dataclasses
 from contextlib import nullcontext
 
-_COMPOUND = ("aten._log_softmax.default", "aten.log_softmax.int", "aten.log_softmax.default",
-             "aten.logsumexp.default")
+# compound targets -> whether the op is a log_softmax (else logsumexp)
+_COMPOUNDS = {"aten._log_softmax.default": True, "aten.log_softmax.int": True,
+              "aten.log_softmax.default": True, "aten.logsumexp.default": False}
+MARK = "neptune_lowering"
 
 
-def _name_of(target) -> str:
-    text = str(target)
-    return text[len("aten."):].split(".")[0] if text.startswith("aten.") else text.split(".")[0]
+class _Ref(str):
+    """In a step's argument template: the value named by an earlier step (or x / dim)."""
 
 
-def _is_compound(node) -> bool:
-    return node.op == "call_function" and str(node.target) in _COMPOUND
+def _bind(template, env):
+    if isinstance(template, _Ref):
+        return env[template]
+    if isinstance(template, (tuple, list)):
+        return type(template)(_bind(item, env) for item in template)
+    return template
 
 
-def _value(node):
-    meta = getattr(node, "meta", {})
-    value = meta.get("val")
-    return meta.get("example_value") if value is None else value
+_X, _DIM = _Ref("x"), _Ref("dim")
+_LSE_STEPS = (
+    ("amax.default", "m", (_X, [_DIM], True)),
+    ("abs.default", "abs_m", (_Ref("m"),)),
+    ("eq.Scalar", "infinite", (_Ref("abs_m"), float("inf"))),
+    ("where.ScalarSelf", "m_safe", (_Ref("infinite"), 0.0, _Ref("m"))),
+    ("sub.Tensor", "centred", (_X, _Ref("m_safe"))),
+    ("exp.default", "e", (_Ref("centred"),)),
+    ("sum.dim_IntList", "s", (_Ref("e"), [_DIM], True)),
+    ("log.default", "lg", (_Ref("s"),)),
+    ("add.Tensor", "lse", (_Ref("m_safe"), _Ref("lg"))),
+)
+_LOG_SOFTMAX_TAIL = (
+    ("eq.Scalar", "posinf_row", (_Ref("lse"), float("inf"))),
+    ("sub.Tensor", "readout", (_X, _Ref("lse"))),
+    ("where.ScalarSelf", "log_out", (_Ref("posinf_row"), float("nan"), _Ref("readout"))),
+)
 
 
-def _arg(node, name, position, default=None):
-    return node.kwargs.get(name, node.args[position] if len(node.args) > position else default)
+def _program(dtype, output_dtype, *, log_softmax: bool, keepdim: bool):
+    """[(aten overload path, value name, argument template, kwargs)] ending in the result."""
+    import torch
+
+    accumulate = torch.float32 if dtype in (torch.float16, torch.bfloat16) else dtype
+    steps = []
+    if accumulate != dtype:
+        steps.append(("_to_copy.default", "x", (_X,), {"dtype": accumulate}))
+    steps += [(path, name, args, {}) for path, name, args in _LSE_STEPS]
+    if log_softmax:
+        steps += [(path, name, args, {}) for path, name, args in _LOG_SOFTMAX_TAIL]
+    elif not keepdim:
+        steps.append(("squeeze.dim", "squeezed", (_Ref("lse"), _DIM), {}))
+    if output_dtype != accumulate:
+        steps.append(("_to_copy.default", "out", (_Ref(steps[-1][1]),), {"dtype": output_dtype}))
+    return steps
 
 
 def _aten(path: str):
@@ -45,63 +89,39 @@ def _aten(path: str):
     return op
 
 
-def _steps(dtype, output_dtype, *, log_softmax: bool, keepdim: bool):
-    """[(aten overload path, name, args(env), kwargs)], result name.  Accumulation is fp32 for
-    16-bit inputs; casts stay explicit region boundaries."""
-    import torch
-
-    acc = torch.float32 if dtype in (torch.float16, torch.bfloat16) else dtype
-    steps = []
-    if dtype != acc:
-        steps.append(("_to_copy.default", "x", lambda e: (e["x"],), {"dtype": acc}))
-    steps += [
-        ("amax.default", "m", lambda e: (e["x"], [e["dim"]], True), {}),
-        ("abs.default", "abs_m", lambda e: (e["m"],), {}),
-        ("eq.Scalar", "infinite", lambda e: (e["abs_m"], float("inf")), {}),
-        ("where.ScalarSelf", "m_safe", lambda e: (e["infinite"], 0.0, e["m"]), {}),
-        ("sub.Tensor", "centred", lambda e: (e["x"], e["m_safe"]), {}),
-        ("exp.default", "e", lambda e: (e["centred"],), {}),
-        ("sum.dim_IntList", "s", lambda e: (e["e"], [e["dim"]], True), {}),
-        ("log.default", "lg", lambda e: (e["s"],), {}),
-        ("add.Tensor", "lse", lambda e: (e["m_safe"], e["lg"]), {}),
-    ]
-    result = "lse"
-    if log_softmax:
-        steps += [
-            ("eq.Scalar", "posinf_row", lambda e: (e["lse"], float("inf")), {}),
-            ("sub.Tensor", "readout", lambda e: (e["x"], e["lse"]), {}),
-            ("where.ScalarSelf", "log_out", lambda e: (e["posinf_row"], float("nan"), e["readout"]), {}),
-        ]
-        result = "log_out"
-    elif not keepdim:
-        steps.append(("squeeze.dim", "squeezed", lambda e: (e["lse"], e["dim"]), {}))
-        result = "squeezed"
-    if output_dtype != acc:
-        steps.append(("_to_copy.default", "out", lambda e, key=result: (e[key],), {"dtype": output_dtype}))
-        result = "out"
-    return steps, result
-
-
-def _fake_run(value, dim, *, output_dtype, log_softmax, keepdim) -> dict:
-    """Metadata of every step, computed by torch on Fake/meta tensors (no real arithmetic)."""
-    import torch
-
-    if type(value).__name__ != "FakeTensor" and not value.is_meta:
-        value = torch.empty_strided(value.shape, value.stride(), dtype=value.dtype, device="meta")
-    steps, result = _steps(value.dtype, output_dtype, log_softmax=log_softmax, keepdim=keepdim)
-    env = {"x": value, "dim": dim}
-    with getattr(value, "fake_mode", None) or nullcontext():
-        for path, name, build, kwargs in steps:
-            env[name] = _aten(path)(*build(env), **kwargs)
-    env["out"] = env[result]
+def _play(steps, env, apply):
+    """Run `steps` over env (which holds x and dim); apply(op, args, kwargs, name) gives each
+    step's value.  Returns env with every step's value under its name."""
+    for path, name, template, kwargs in steps:
+        env[name] = apply(_aten(path), _bind(template, env), kwargs, name)
     return env
 
 
-def _simulatable(value) -> bool:
-    """Fake/meta metadata, or a tiny real CPU example; never GPU work."""
+def _value(node):
+    meta = getattr(node, "meta", {})
+    held = meta.get("val")
+    return meta.get("example_value") if held is None else held
+
+
+def _is_fake_or_meta(value) -> bool:
+    return type(value).__name__ == "FakeTensor" or bool(getattr(value, "is_meta", False))
+
+
+def _as_metadata(value):
+    """value itself when it is Fake/meta; otherwise an empty meta tensor of its layout."""
+    import torch
+
+    if _is_fake_or_meta(value):
+        return value
+    return torch.empty_strided(value.shape, value.stride(), dtype=value.dtype, device="meta")
+
+
+def _metadata_only(value) -> bool:
+    """Lowering computes metadata with torch: it accepts Fake/meta values, and real values
+    only as tiny CPU examples (never GPU work in this pass)."""
     if value is None:
         return False
-    if type(value).__name__ == "FakeTensor" or getattr(value, "is_meta", False):
+    if _is_fake_or_meta(value):
         return True
     if getattr(getattr(value, "device", None), "type", None) != "cpu":
         return False
@@ -109,133 +129,182 @@ def _simulatable(value) -> bool:
     return callable(numel) and numel() <= 4096
 
 
-def _trial_graph(gm):
-    import torch.fx as fx
+@dataclasses.dataclass
+class _Compound:
+    """One lowerable call: what the expansion needs to know about it."""
 
-    return fx.GraphModule(gm, copy.deepcopy(gm.graph))
-
-
-def _commit(gm, trial):
-    """Install trial's graph into gm; a failing recompile restores gm exactly."""
-    saved = gm.__dict__.copy()
-    cls = type(gm)
-    generated = {key: cls.__dict__.get(key) for key in ("forward", "_wrapped_call")}
-    try:
-        gm.graph = trial.graph
-    except Exception:
-        gm.__dict__.clear()
-        gm.__dict__.update(saved)
-        gm.graph.owning_module = gm
-        trial.graph.owning_module = trial
-        for key, value in generated.items():
-            if value is not None:
-                setattr(cls, key, value)
-            elif key in cls.__dict__:
-                delattr(cls, key)
-        raise
+    node: object
+    x: object
+    dim: int
+    keepdim: bool
+    log_softmax: bool
+    cast_to: object          # log_softmax(x, dim, dtype): the dtype x converts to first
+    source: object           # metadata of x
+    output: object           # metadata of the call's result
 
 
-def _expand_node(gm, node) -> bool:
+def is_compound(node) -> bool:
+    return node.op == "call_function" and str(node.target) in _COMPOUNDS
+
+
+def is_log_softmax(node) -> bool:
+    return is_compound(node) and _COMPOUNDS[str(node.target)]
+
+
+def _schema_name(node) -> str:
+    return str(node.target).split(".")[1]
+
+
+def _argument(node, name, position, default=None):
+    if name in node.kwargs:
+        return node.kwargs[name]
+    return node.args[position] if len(node.args) > position else default
+
+
+def _describe(node):
+    """The _Compound for node, or None when it is not one this pass lowers."""
     import torch
 
-    if not _is_compound(node):
-        return False
-    is_log = _name_of(node.target) in ("_log_softmax", "log_softmax")
-    if _name_of(node.target) == "_log_softmax" and _arg(node, "half_to_float", 2, False) is not False:
-        return False
-    x = _arg(node, "self", 0)
+    if not is_compound(node):
+        return None
+    schema = _schema_name(node)
+    if schema == "_log_softmax" and _argument(node, "half_to_float", 2, False) is not False:
+        return None
+    floats = (torch.float32, torch.float16, torch.bfloat16)
+    x = _argument(node, "self", 0)
     source, output = _value(x), _value(node)
-    allowed = (torch.float32, torch.float16, torch.bfloat16)
-    if (source is None or output is None or getattr(source, "dtype", None) not in allowed
-            or getattr(output, "dtype", None) not in allowed or not _simulatable(source)):
-        return False
+    if getattr(source, "dtype", None) not in floats or getattr(output, "dtype", None) not in floats:
+        return None
+    if not _metadata_only(source):
+        return None
     rank = len(source.shape)
-    dim = _arg(node, "dim", 1)
-    if _name_of(node.target) == "logsumexp" and isinstance(dim, (tuple, list)):
+    dim = _argument(node, "dim", 1)
+    if schema == "logsumexp" and isinstance(dim, (tuple, list)):
         dim = dim[0] if len(dim) == 1 else None
     if type(dim) is not int or rank < 1 or dim not in (-1, rank - 1):
-        return False
-    if type(source.shape[-1]) is int and source.shape[-1] <= 0:
-        return False
-    keepdim = True if is_log else _arg(node, "keepdim", 2, False)
+        return None
+    width = source.shape[-1]
+    if type(width) is int and width <= 0:
+        return None
+    log_softmax = is_log_softmax(node)
+    keepdim = True if log_softmax else _argument(node, "keepdim", 2, False)
     if type(keepdim) is not bool:
+        return None
+    cast_to = _argument(node, "dtype", 2) if schema == "log_softmax" else None
+    if (cast_to or source.dtype) not in floats or output.dtype != (cast_to or source.dtype):
+        return None
+    return _Compound(node, x, dim, keepdim, log_softmax, cast_to, source, output)
+
+
+def _expand(gm, node) -> bool:
+    """Replace node by its expansion in gm's graph; False (and no edit) when it does not lower
+    or the expansion's metadata would not reproduce the node's output shape."""
+    call = _describe(node)
+    if call is None:
         return False
-    # log_softmax(x, dim, dtype) converts before any arithmetic
-    requested = _arg(node, "dtype", 2) if _name_of(node.target) == "log_softmax" else None
-    effective = requested or source.dtype
-    if effective not in allowed or output.dtype != effective:
+    fake_x = call.source
+    if call.cast_to is not None:
+        with getattr(call.source, "fake_mode", None) or nullcontext():
+            fake_x = _aten("_to_copy.default")(_as_metadata(call.source), dtype=call.cast_to)
+    steps = _program(fake_x.dtype, call.output.dtype, log_softmax=call.log_softmax,
+                     keepdim=call.keepdim)
+    start = _as_metadata(fake_x)
+    with getattr(start, "fake_mode", None) or nullcontext():
+        fake = _play(steps, {"x": start, "dim": call.dim}, lambda op, args, kw, name: op(*args, **kw))
+    result = steps[-1][1]
+    if [str(size) for size in fake[result].shape] != [str(size) for size in call.output.shape]:
         return False
-    fake_source = source
-    if requested is not None:
-        with getattr(source, "fake_mode", None) or nullcontext():
-            if type(source).__name__ != "FakeTensor" and not source.is_meta:
-                fake_source = torch.empty_strided(source.shape, source.stride(), dtype=source.dtype,
-                                                  device="meta")
-            fake_source = _aten("_to_copy.default")(fake_source, dtype=requested)
-    fake = _fake_run(fake_source, dim, output_dtype=output.dtype, log_softmax=is_log, keepdim=keepdim)
-    if tuple(map(str, fake["out"].shape)) != tuple(map(str, output.shape)):
-        return False
-    steps, result = _steps(effective, output.dtype, log_softmax=is_log, keepdim=keepdim)
     graph = gm.graph
+
+    def emit(op, args, kwargs, name):
+        created = graph.call_function(op, args=args, kwargs=kwargs)
+        created.meta.update({"val": fake[name], MARK: node.name})
+        return created
+
     with graph.inserting_before(node):
-        env = {"x": x, "dim": dim}
-        if requested is not None:
-            cast = graph.call_function(_aten("_to_copy.default"), args=(x,), kwargs={"dtype": requested})
-            cast.meta.update(val=fake_source, neptune_lowering=node.name)
-            env["x"] = cast
-        for path, name, build, kwargs in steps:
-            call = graph.call_function(_aten(path), args=build(env), kwargs=kwargs)
-            call.meta.update(val=fake[name], neptune_lowering=node.name)
-            env[name] = call
+        env = {"x": call.x, "dim": call.dim}
+        if call.cast_to is not None:
+            env["x"] = graph.call_function(_aten("_to_copy.default"), args=(call.x,),
+                                           kwargs={"dtype": call.cast_to})
+            env["x"].meta.update({"val": fake_x, MARK: node.name})
+        _play(steps, env, emit)
     node.replace_all_uses_with(env[result])
     graph.erase_node(node)
     return True
 
 
-def lower_compound(gm, nodes=None) -> int:
-    """Expand the supported compound nodes (all, or the given nodes / names) in place.
-    Returns how many were expanded; on any failure `gm` is left untouched and 0 returned."""
+def fork_graph(gm):
+    """A GraphModule with a private copy of gm's graph; parameters and buffers are shared."""
+    import torch.fx as fx
+
+    return fx.GraphModule(gm, copy.deepcopy(gm.graph))
+
+
+def install(gm, trial) -> None:
+    """gm takes trial's (already compiled) graph.  Should gm's recompile fail, gm gets its
+    previous graph (and code) back and the error propagates."""
+    previous = gm.graph
+    try:
+        gm.graph = trial.graph
+    except Exception:
+        trial.graph.owning_module = trial
+        gm.graph = previous
+        raise
+
+
+def _names(gm, nodes):
     if nodes is None:
-        names = {n.name for n in gm.graph.nodes if _is_compound(n)}
-    elif isinstance(nodes, str) or hasattr(nodes, "op"):
-        names = {nodes if isinstance(nodes, str) else nodes.name}
-    else:
-        names = {n if isinstance(n, str) else n.name for n in nodes}
-    if not names:
+        return {n.name for n in gm.graph.nodes if is_compound(n)}
+    if isinstance(nodes, str) or hasattr(nodes, "op"):
+        nodes = (nodes,)
+    return {n if isinstance(n, str) else n.name for n in nodes}
+
+
+def lower_compound(gm, nodes=None) -> int:
+    """Expand every supported compound node of gm, or those given (nodes or names), in place.
+    No benefit gate.  Returns how many were expanded; on any failure gm is untouched and 0 is
+    returned."""
+    wanted = _names(gm, nodes)
+    if not wanted:
         return 0
     try:
-        trial = _trial_graph(gm)
-        count = sum(_expand_node(trial, n) for n in list(trial.graph.nodes) if n.name in names)
-        if not count:
-            return 0
-        trial.graph.lint()
-        trial.recompile()
-        _commit(gm, trial)
+        trial = fork_graph(gm)
+        count = 0
+        for node in list(trial.graph.nodes):
+            if node.name in wanted and _expand(trial, node):
+                count += 1
+        if count:
+            trial.graph.lint()
+            trial.recompile()
+            install(gm, trial)
         return count
-    except Exception:  # noqa: BLE001 -- an unsupported trial never mutates the caller
+    except Exception:  # noqa: BLE001 -- an unsupported trial never changes the caller's graph
         return 0
 
 
-def lower_if_it_helps(gm, values=None) -> int:
-    """Lower each compound node only when its own expansion becomes an eligible region."""
+def grew_eligible_region(gm, name, values=None) -> bool:
+    """True when gm (after lowering compound node `name`) holds an eligible region rooted in
+    and built from that node's expansion, and `rewrite` would fuse a region of gm."""
     from neptune_recognize.match import recognize_regions
     from neptune_recognize.rewrite import region_contract, would_rewrite
 
+    matches, _ = recognize_regions(gm, values)
+    own = [m for m in matches if m.region_root.meta.get(MARK) == name
+           and any(n.meta.get(MARK) == name for n in m.region_nodes)]
+    return any(region_contract(m)[1] is None for m in own) and would_rewrite(gm, values)[0]
+
+
+def lower_if_it_helps(gm, values=None) -> int:
+    """Lower each compound node only when its own expansion becomes an eligible region (another
+    region of the graph cannot vouch for it).  No kernel generation and no dead-code removal.
+    Returns how many nodes were lowered."""
     lowered = 0
-    for name in [n.name for n in gm.graph.nodes if _is_compound(n)]:
+    for name in [n.name for n in gm.graph.nodes if is_compound(n)]:
         try:
-            trial = _trial_graph(gm)
-            if not lower_compound(trial, nodes=name):
-                continue
-            matches, _ = recognize_regions(trial, values)
-            eligible = any(
-                m.region_root.meta.get("neptune_lowering") == name
-                and any(n.meta.get("neptune_lowering") == name for n in m.region_nodes)
-                and region_contract(m)[1] is None for m in matches)
-            if not eligible or not would_rewrite(trial, values)[0]:
-                continue
-            _commit(gm, trial)
-            lowered += 1
+            trial = fork_graph(gm)
+            if lower_compound(trial, nodes=name) and grew_eligible_region(trial, name, values):
+                install(gm, trial)
+                lowered += 1
         except Exception:  # noqa: BLE001 -- each node is its own transaction
             continue
     return lowered

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import dataclasses
 import functools
+import math
 
 import sympy as sp
 
@@ -353,25 +354,25 @@ def _aten_arguments(node, target):
 
 
 def _structured_cast(node, dtype):
-    """The source of a pure dtype conversion to `dtype` (same device/layout/shape), else None."""
+    """The input node of `node` when node converts it to `dtype` and changes nothing else (same
+    device, layout and shape; default pinning and memory format), else None."""
     import torch
 
-    bound = _aten_arguments(node, torch.ops.aten._to_copy.default)
-    if bound is None:
-        bound = _aten_arguments(node, torch.ops.aten.to.dtype)
-        if bound is not None:
-            bound = {"device": None, "layout": None, "pin_memory": None, **bound}
+    aten = torch.ops.aten
+    bound = _aten_arguments(node, aten._to_copy.default) or _aten_arguments(node, aten.to.dtype)
     if bound is None or bound["dtype"] != dtype:
         return None
-    src, out = _tensor_value(bound["self"]), _tensor_value(node)
-    if src is None or out is None:
+    source, result = _tensor_value(bound["self"]), _tensor_value(node)
+    if source is None or result is None:
         return None
-    if (src.device != out.device or src.layout != out.layout or not _same_shape(src.shape, out.shape)
-            or bound["device"] not in (None, src.device) or bound["layout"] not in (None, src.layout)
-            or bound["pin_memory"] not in (None, False)
-            or bound["memory_format"] not in (None, torch.preserve_format)):
+    # aten.to.dtype has no device / layout / pin_memory arguments: absent means unchanged
+    requested = (bound.get("device"), bound.get("layout"), bound.get("pin_memory"), bound["memory_format"])
+    unchanged = (source.device, source.layout, False, torch.preserve_format)
+    if any(want is not None and want != keep for want, keep in zip(requested, unchanged)):
         return None
-    return bound["self"]
+    if source.device != result.device or source.layout != result.layout:
+        return None
+    return bound["self"] if _same_shape(source.shape, result.shape) else None
 
 
 def _square_of(node, z) -> bool:
@@ -487,36 +488,36 @@ def _structured_boundary_value(gm, node):
     return obj if isinstance(obj, torch.Tensor) else None
 
 
-def _segment_structured_candidate(root):
-    """torch.segment_reduce(data, sum|mean, lengths=|offsets=, axis=0) with a finite initial."""
-    import math
+_SEGMENT_ASSUMPTIONS = (
+    "finite real data and finite reachable accumulation",
+    "readonly legal descriptors: nonnegative lengths with checked coverage unless unsafe, or monotone offsets within data bounds",
+    "initial is None or a finite scalar; mean empty segment with initial=None returns NaN",
+    "source unsafe is reused, not a proof of valid descriptors",
+)
 
+
+def _segment_structured_candidate(root):
+    """A Match for torch.segment_reduce(data, 'sum' | 'mean', lengths= xor offsets=, axis=0)
+    with an explicit bool `unsafe` and `initial` None or finite; None for anything else."""
     import torch
 
     bound = _aten_arguments(root, torch.ops.aten.segment_reduce.default)
-    if bound is None or bound["reduce"] not in ("sum", "mean") or bound["axis"] != 0:
+    if bound is None:
         return None
-    if bound["indices"] is not None or (bound["lengths"] is None) == (bound["offsets"] is None):
-        return None
+    given = [key for key in ("lengths", "offsets") if bound[key] is not None]
     initial = bound["initial"]
-    if initial is not None and (type(initial) not in (float, int) or not math.isfinite(initial)):
+    initial_ok = initial is None or (type(initial) in (int, float) and math.isfinite(initial))
+    if (bound["reduce"] not in ("sum", "mean") or bound["axis"] != 0 or bound["indices"] is not None
+            or len(given) != 1 or not initial_ok or type(bound["unsafe"]) is not bool):
         return None
-    if type(bound["unsafe"]) is not bool:
-        return None
-    offsets = bound["offsets"] is not None
-    descriptor = bound["offsets"] if offsets else bound["lengths"]
-    return Match(
-        bound["data"], "segment_" + bound["reduce"],
-        {"initial": None if initial is None else float(initial), "offsets": offsets,
-         "unsafe": bound["unsafe"]},
-        region_root=root, region_nodes=(root,),
-        proof_kind="exact-structured-real-algebra-with-explicit-rounding",
-        domain_assumptions=("finite real data and finite reachable accumulation",
-                            "readonly legal descriptors: nonnegative lengths with checked coverage unless unsafe, or monotone offsets within data bounds",
-                            "initial is None or a finite scalar; mean empty segment with initial=None returns NaN",
-                            "source unsafe is reused, not a proof of valid descriptors"),
-        input_nodes=(bound["data"], descriptor), kind="structured", operation="segment_pool",
-        metadata={"numerical_stages": "input_round"})
+    params = {"initial": None if initial is None else float(initial),
+              "offsets": given[0] == "offsets", "unsafe": bound["unsafe"]}
+    return Match(bound["data"], f"segment_{bound['reduce']}", params, region_root=root,
+                 region_nodes=(root,),
+                 proof_kind="exact-structured-real-algebra-with-explicit-rounding",
+                 domain_assumptions=_SEGMENT_ASSUMPTIONS,
+                 input_nodes=(bound["data"], bound[given[0]]), kind="structured",
+                 operation="segment_pool", metadata={"numerical_stages": "input_round"})
 
 
 def recognize_structured_regions(gm, capabilities=("rms_norm", "segment_pool")):

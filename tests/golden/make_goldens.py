@@ -85,7 +85,20 @@ def main():
         "partition_data": [-3.0, 0.0, 2.0, 1.0, -1.0, 0.0, 5.0], "partition_block": 2, "rtol": 2e-6, "atol": 1e-6,
         "zero_floor_data": [0.0, 0.5e-30, 0.5e-30],
         "zero_floor_skeletons": ["stable_l2", "linear_attn", "sumsq_div"]}, indent=1))
-    # 7. segment pooling: tests/test_autotune.py:793-833, expected from torch.segment_reduce (CPU)
+    # 7. declared parameter defaults per skeleton, as the reference's registry states them
+    #    (neptune_codegen/library.py:27-28 logsumexp, :55 decay_renorm, :67-68 softcap_lse,
+    #    :87-88 rmsnorm_max, :109-110 lse_biased, :170-175 lse_scaled; no params for stable_l2,
+    #    linear_attn, sumsq_div, variance, std) with param_defaults' 1.0 fallback for an
+    #    undeclared scalar and intrinsic ncols left out (neptune_codegen/skeleton.py:255-267)
+    (HERE / "param_defaults.json").write_text(json.dumps({
+        "source": "reference neptune_codegen/library.py:19-177 declarations, "
+                  "skeleton.py:255-267 fallback rule",
+        "defaults": {"logsumexp": {"tiny": 0.0}, "stable_l2": {}, "linear_attn": {},
+                     "decay_renorm": {"N": 1.0}, "softcap_lse": {"beta": 1.0, "tiny": 0.0},
+                     "rmsnorm_max": {"eps": 1.0}, "sumsq_div": {},
+                     "lse_biased": {"alpha": 1.0, "tiny": 0.0}, "variance": {}, "std": {},
+                     "lse_scaled": {"T": 2.0, "tiny": 0.0}}}, indent=1))
+    # 8. segment pooling: tests/test_autotune.py:793-833, expected from torch.segment_reduce (CPU)
     import torch
 
     cases = []

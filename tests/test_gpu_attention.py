@@ -14,6 +14,12 @@ from neptune_codegen.emitters import BASE_OPTIONS, kernel_header
 from oracle import references as R
 
 pytestmark = pytest.mark.gpu
+# The fold's row sum l adds the fp16-rounded P values that the P.V MFMA multiplies (so O is
+# normalised by exactly the weights it used).  A normal fp16 rounding errs by at most 2^-11
+# relative (fp16's unit roundoff); a subnormal one (P < 2^-14) by at most 2^-25 absolute.  The
+# row's largest P is >= 1, so l >= 1, and for at most 4096 keys the logsumexp m + log(l) is
+# within -log(1 - 2^-11) + 4096 * 2^-25 (+ fp32 rounding of m + log l) of the fp32 value.
+LSE_ATOL = -math.log1p(-2.0 ** -11) + 4096 * 2.0 ** -25 + 1e-6
 
 
 def _dev():
@@ -72,7 +78,7 @@ def test_attention_parity(shape, causal):
     s = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) / math.sqrt(D)
     if causal:
         s = s.masked_fill(~torch.ones(Sq, Sk, dtype=torch.bool).tril(0), float("-inf"))
-    torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=1e-5, atol=LSE_ATOL)
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -112,20 +118,6 @@ def test_attention_strided_layout_and_scale():
                            vs.to(dev).transpose(1, 2), scale=0.05, causal=True)
     want = R.attention_reference(q, k, v, scale=0.05, causal=True)
     torch.testing.assert_close(got.cpu().float(), want.float(), rtol=1.6e-2, atol=1e-3)
-
-
-def test_attention_cfg5_shape_head_subset():
-    """cfg5 (B=4, H=32, S=4096, D=128, causal) on the GPU; two heads checked on the CPU."""
-    dev = _dev()
-    g = torch.Generator().manual_seed(5)
-    shape = (4, 32, 4096, 128)
-    q, k, v = (torch.randn(*shape, generator=g).bfloat16() for _ in range(3))
-    _say("attention cfg5 [4,32,4096,128] causal")
-    got = CG.run_attention(q.to(dev), k.to(dev), v.to(dev), causal=True).cpu()
-    for b, h in ((0, 0), (3, 31)):
-        want = R.attention_reference(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1])
-        torch.testing.assert_close(got[b:b + 1, h:h + 1].float(), want.float(), rtol=1.6e-2, atol=1e-3)
-    assert torch.isfinite(got.float()).all()
 
 
 def test_attention_custom_op():

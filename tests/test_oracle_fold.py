@@ -96,12 +96,21 @@ def test_closed_forms(name, plan):
     np.testing.assert_allclose(got, want, rtol=R.summation_tolerance(torch.float32, 300), atol=1e-6)
 
 
-def test_reference_defaults_match_declared_defaults():
-    """The oracle's parameter defaults equal the skeleton registry's declared ones."""
+def test_defaults_match_the_reference_declarations():
+    """The oracle's parameter defaults and the product registry's `param_defaults` both equal
+    the defaults the reference declares per skeleton (golden transcribed from
+    neptune_codegen/library.py:19-177 with skeleton.py:255-267's 1.0 fallback)."""
+    import json
+    import pathlib
+
     import neptune_codegen as CG
 
-    for name in OF.SPECS:
-        for arg, value in CG.param_defaults(name).items():
+    golden = json.loads((pathlib.Path(__file__).parent / "golden" / "param_defaults.json").read_text())
+    declared = golden["defaults"]
+    assert set(declared) == set(CG.supported()) == set(OF.SPECS)
+    for name, values in declared.items():
+        assert CG.param_defaults(name) == values, name
+        for arg, value in values.items():
             assert OF.DEFAULTS[arg] == value, (name, arg)
 
 
