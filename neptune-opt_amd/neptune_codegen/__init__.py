@@ -19,7 +19,7 @@ from neptune_codegen.attention import as_attention_op, attention_fold, run_atten
 from neptune_codegen.autotune import best_config, machine_key, op_key, parameter_tag
 from neptune_codegen.emitters import (check_supported, derived_producer_expr, emit_fold_policy,
                                       emit_kernel_source, emit_rms_state_source,
-                                      emit_segment_source)
+                                      emit_segment_source, param_bindings)
 from neptune_codegen.skeleton import (NEGATIVE_CONTROLS, SKELETONS, STATE_REDUCTIONS,
                                       NumericalContract, Skeleton, StateField, StateReduction,
                                       all_registered, param_defaults, register,
@@ -55,6 +55,7 @@ __all__ = [
     "StateCertificate",
     "to_hip", "TranslationError", "check_supported", "derived_producer_expr",
     "emit_fold_policy", "emit_kernel_source", "emit_rms_state_source", "emit_segment_source",
+    "param_bindings",
     "MAX_SPLIT_PARTS", "validate_plan", "split_launch_shape", "compile_skeleton",
     "compile_state_reduction", "generated_path", "launch_reduction", "launch_rms_norm", "run",
     "run_rms_norm", "run_l2_normalize", "validate_rms_inputs", "validate_l2_inputs",

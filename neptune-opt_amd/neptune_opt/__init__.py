@@ -47,23 +47,36 @@ def _capabilities(capabilities: Iterable[str]) -> tuple:
     return _bounded_names(capabilities, ("rms_norm", "segment_pool"), _CAPABILITY_MESSAGES)
 
 
+def _is_count(value, least) -> bool:
+    return type(value) is int and value >= least
+
+
+# apply's argument checks, in order: (is the argument acceptable, ValueError text)
+_ARGUMENT_CHECKS = (
+    (lambda o: o["max_regions"] is None or _is_count(o["max_regions"], 1),
+     "max_regions must be a positive integer or None"),
+    (lambda o: all(math.isfinite(t) and t >= 0 for t in (o["rtol"], o["atol"])),
+     "verification tolerances must be finite and nonnegative"),
+    (lambda o: o["max_ulps"] is None or _is_count(o["max_ulps"], 0),
+     "max_ulps must be a nonnegative integer or None"),
+    (lambda o: o["cases"] is None or isinstance(o["cases"], Sequence),
+     "verification_inputs must be a sequence of argument tuples"),
+    (lambda o: o["cases"] is None or all(isinstance(c, tuple) for c in o["cases"]),
+     "each verification_inputs sample must be an argument tuple"),
+)
+
+
 def _checked_options(plan, capabilities, max_regions, rtol, atol, max_ulps, verification_inputs):
     """(capabilities, Tolerance); ValueError names the first bad argument."""
     from neptune_codegen.template import validate_plan
 
     validate_plan(plan)
     capabilities = _capabilities(capabilities)
-    if max_regions is not None and (type(max_regions) is not int or max_regions <= 0):
-        raise ValueError("max_regions must be a positive integer or None")
-    if not all(math.isfinite(t) and t >= 0 for t in (rtol, atol)):
-        raise ValueError("verification tolerances must be finite and nonnegative")
-    if max_ulps is not None and (type(max_ulps) is not int or max_ulps < 0):
-        raise ValueError("max_ulps must be a nonnegative integer or None")
-    if verification_inputs is not None:
-        if not isinstance(verification_inputs, Sequence):
-            raise ValueError("verification_inputs must be a sequence of argument tuples")
-        if not all(isinstance(case, tuple) for case in verification_inputs):
-            raise ValueError("each verification_inputs sample must be an argument tuple")
+    given = {"max_regions": max_regions, "rtol": rtol, "atol": atol, "max_ulps": max_ulps,
+             "cases": verification_inputs}
+    for acceptable, message in _ARGUMENT_CHECKS:
+        if not acceptable(given):
+            raise ValueError(message)
     return capabilities, Tolerance(rtol, atol, max_ulps)
 
 

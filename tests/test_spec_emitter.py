@@ -155,3 +155,15 @@ def test_supported_and_registry():
         CG.register(CG.Skeleton(name="logsumexp", g=c_sym, finalize=CG._FINAL_ACC))
     assert CG.param_defaults("lse_scaled") == {"T": 2.0, "tiny": 0.0}
     assert CG.param_defaults("rmsnorm_max") == {"eps": 1.0}
+
+
+def test_param_bindings_is_exported_and_bakes_fp32_literals():
+    """The reference exports param_bindings from neptune_codegen (__init__.py:147-156): scalar
+    parameters become source literals, intrinsic row lengths the kernel's n."""
+    import neptune_codegen as CG
+
+    bound = CG.param_bindings(CG.SKELETONS["lse_scaled"], {"T": 2.0, "tiny": 0.0})
+    assert {str(k): v for k, v in bound.items()} == {"T": "0x1.0000000000000p+1f", "tiny": "0.0f"}
+    assert {str(k): v for k, v in CG.param_bindings(CG.SKELETONS["variance"]).items()} == {"N": "n"}
+    with pytest.raises(KeyError, match="beta"):
+        CG.param_bindings(CG.SKELETONS["softcap_lse"], {"tiny": 0.0})
