@@ -23,6 +23,9 @@
  *   nep_launch_packed        the same launch with the arguments already packed into one kernarg
  *                            image (what Triton's generated launcher builds per call); the host
  *                            cost per launch is one call, with no per-argument pointer array.
+ *   nep_fold_split           replaces the split branch of launch_reduction
+ *                            (template.py:380-390, kernels template.py:137-165): a generated
+ *                            fold's partial and merge kernels over a caller-owned workspace.
  *   nep_last_error           the text the reference surfaces through Python exceptions; it
  *                            carries the HIP error name so that fatal-error classification by
  *                            message (neptune_opt/ab.py:23-44) keeps working.
@@ -106,6 +109,29 @@ int nep_launch(uint64_t kernel, const uint32_t grid[3], const uint32_t block[3],
  */
 int nep_launch_packed(uint64_t kernel, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block,
                       uint32_t lds_bytes, void* stream, const void* args, size_t nbytes);
+
+/*
+ * Bytes of workspace nep_fold_split needs for `rows` rows of `nparts` partials: four arrays
+ * of rows*nparts 4-byte fields (running max m, accumulator acc, seen flag, status bits).
+ */
+size_t nep_fold_split_workspace_bytes(int64_t rows, int64_t nparts);
+
+/*
+ * The split plan of one scalar fold on `stream`.  `partial_kernel` and `merge_kernel` are the
+ * generated unit's "<name>_partial_<variant>" and "<name>_merge_<dtype>" kernels
+ * (nep_get_kernel); x is [rows, ncols] with strides (row_stride, col_stride) in elements, out
+ * holds `rows` results in x's dtype.  nparts must be ceil(ncols / block) (block a power of
+ * two, nparts <= 4096: split_launch_shape, template.py:114-125); partial_threads and
+ * parts_per_workgroup are the partial kernel's workgroup size and the (row, part) pairs one
+ * workgroup covers (its workgroup size / lanes per part).  `workspace` is device memory of at
+ * least nep_fold_split_workspace_bytes(rows, nparts) bytes, owned by the caller and not read
+ * before the partial kernel writes it.  Two launches, no synchronisation, no allocation.
+ */
+int nep_fold_split(uint64_t partial_kernel, uint64_t merge_kernel, const void* x, void* out,
+                   int64_t rows, int64_t ncols, int64_t row_stride, int64_t col_stride,
+                   int64_t nparts, int64_t block, uint32_t partial_threads,
+                   uint32_t parts_per_workgroup, void* workspace, size_t workspace_bytes,
+                   void* stream);
 
 /* Name of the current device's ISA (e.g. "gfx950:sramecc+:xnack-") into buf. */
 int nep_device_arch(char* buf, size_t buf_len);

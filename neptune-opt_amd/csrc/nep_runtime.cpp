@@ -264,3 +264,114 @@ int nep_device_arch(char* buf, size_t buf_len) {
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- split plan, typed
+// The reference's split branch of launch_reduction (neptune_codegen/template.py:380-390):
+// the partial kernel writes one exact chunk state (m, acc, seen, status) per (row, part) into
+// scratch, the merge kernel folds each row's states with merge_state and finalises.
+namespace {
+
+// argument images of the generated split kernels (emitters.py's _fold_kernel signatures)
+struct SplitPartialArgs {
+  const void* x;
+  float* pm;
+  float* pa;
+  int* pv;
+  int* ps;
+  long long rows, ncols, stride_row, stride_col, nparts, block;
+};
+struct SplitMergeArgs {
+  const float* pm;
+  const float* pa;
+  const int* pv;
+  const int* ps;
+  void* out;
+  long long rows, ncols, nparts;
+};
+
+constexpr int64_t kMaxSplitParts = 4096;     // template.py MAX_SPLIT_PARTS
+constexpr uint32_t kMergeRowsPerWorkgroup = 4;   // one wave64 per row, 256-lane workgroups
+
+int launch_image(uint64_t kernel, uint32_t grid, uint32_t block, void* stream, void* image,
+                 size_t size, const char* what) {
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, image, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
+                    HIP_LAUNCH_PARAM_END};
+  hipError_t err = hipModuleLaunchKernel(reinterpret_cast<hipFunction_t>(kernel), grid, 1, 1,
+                                         block, 1, 1, 0, reinterpret_cast<hipStream_t>(stream),
+                                         nullptr, config);
+  return err == hipSuccess ? NEP_OK : hip_fail(err, what);
+}
+
+// Shape checks shared by both entry points; 0 partials (rows == 0) is a valid no-op.
+int check_split(const char* who, uint64_t partial_kernel, uint64_t merge_kernel, const void* x,
+                void* out, int64_t rows, int64_t ncols, int64_t nparts, int64_t block,
+                uint32_t partial_threads, uint32_t parts_per_workgroup) {
+  auto bad = [&](const std::string& why) {
+    return fail(NEP_ERR_INVALID, std::string(who) + ": " + why);
+  };
+  if (partial_kernel == 0 || merge_kernel == 0) return bad("null kernel handle");
+  if (rows < 0 || ncols <= 0) return bad("rows must be >= 0 and ncols > 0");
+  if (rows > 0 && (x == nullptr || out == nullptr)) return bad("null input or output");
+  if (block <= 0 || (block & (block - 1)) != 0) return bad("block must be a positive power of two");
+  if (nparts != (ncols + block - 1) / block)
+    return bad("nparts must be ceil(ncols / block) (split_launch_shape)");
+  if (nparts > kMaxSplitParts) return bad("nparts exceeds the split capacity of 4096 partials");
+  if (partial_threads == 0 || partial_threads > 1024 || partial_threads % 64 != 0)
+    return bad("partial_threads must be a multiple of 64 in [64, 1024]");
+  if (parts_per_workgroup == 0 || parts_per_workgroup > partial_threads)
+    return bad("parts_per_workgroup must be in [1, partial_threads]");
+  if (rows > (int64_t(1) << 40) / nparts) return bad("rows * nparts is too large");
+  return NEP_OK;
+}
+
+int run_split(uint64_t partial_kernel, uint64_t merge_kernel, const void* x, void* out,
+              int64_t rows, int64_t ncols, int64_t row_stride, int64_t col_stride, int64_t nparts,
+              int64_t block, uint32_t partial_threads, uint32_t parts_per_workgroup,
+              void* scratch_base, void* stream) {
+  if (rows == 0) return NEP_OK;
+  const int64_t count = rows * nparts;
+  char* base = static_cast<char*>(scratch_base);
+  float* pm = reinterpret_cast<float*>(base);
+  float* pa = reinterpret_cast<float*>(base + 4 * count);
+  int* pv = reinterpret_cast<int*>(base + 8 * count);
+  int* ps = reinterpret_cast<int*>(base + 12 * count);
+  const int64_t partial_grid = (count + parts_per_workgroup - 1) / parts_per_workgroup;
+  const int64_t merge_grid = (rows + kMergeRowsPerWorkgroup - 1) / kMergeRowsPerWorkgroup;
+  if (partial_grid > 0xffffffffLL || merge_grid > 0xffffffffLL)
+    return fail(NEP_ERR_INVALID, "split: grid exceeds 2^32 - 1 workgroups");
+  SplitPartialArgs pargs{x, pm, pa, pv, ps, rows, ncols, row_stride, col_stride, nparts, block};
+  int rc = launch_image(partial_kernel, static_cast<uint32_t>(partial_grid), partial_threads,
+                        stream, &pargs, sizeof(pargs), "hipModuleLaunchKernel(split partial)");
+  if (rc != NEP_OK) return rc;
+  SplitMergeArgs margs{pm, pa, pv, ps, out, rows, ncols, nparts};
+  return launch_image(merge_kernel, static_cast<uint32_t>(merge_grid), 64 * kMergeRowsPerWorkgroup,
+                      stream, &margs, sizeof(margs), "hipModuleLaunchKernel(split merge)");
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t nep_fold_split_workspace_bytes(int64_t rows, int64_t nparts) {
+  if (rows <= 0 || nparts <= 0) return 0;
+  return static_cast<size_t>(16) * static_cast<size_t>(rows) * static_cast<size_t>(nparts);
+}
+
+int nep_fold_split(uint64_t partial_kernel, uint64_t merge_kernel, const void* x, void* out,
+                   int64_t rows, int64_t ncols, int64_t row_stride, int64_t col_stride,
+                   int64_t nparts, int64_t block, uint32_t partial_threads,
+                   uint32_t parts_per_workgroup, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  int rc = check_split("nep_fold_split", partial_kernel, merge_kernel, x, out, rows, ncols, nparts,
+                       block, partial_threads, parts_per_workgroup);
+  if (rc != NEP_OK) return rc;
+  const size_t need = nep_fold_split_workspace_bytes(rows, nparts);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(NEP_ERR_INVALID, "nep_fold_split: workspace holds " + std::to_string(workspace_bytes) +
+                                     " bytes, the split needs " + std::to_string(need));
+  return run_split(partial_kernel, merge_kernel, x, out, rows, ncols, row_stride, col_stride,
+                   nparts, block, partial_threads, parts_per_workgroup, workspace, stream);
+}
+
+}  // extern "C"
+

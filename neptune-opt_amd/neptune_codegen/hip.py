@@ -20,7 +20,7 @@ CACHE_DIR = PACKAGE_DIR / "_codeobj"
 NEP_OK = 0
 EXPORTED = ("nep_abi_version", "nep_last_error", "nep_compile", "nep_compile_code_object",
             "nep_free", "nep_module_load", "nep_get_kernel", "nep_launch", "nep_launch_packed",
-            "nep_device_arch")
+            "nep_device_arch", "nep_fold_split_workspace_bytes", "nep_fold_split")
 
 _lock = threading.Lock()
 _lib = None
@@ -72,6 +72,13 @@ def load_library(require_torch: bool = True) -> ctypes.CDLL:
         lib.nep_launch_packed.restype = ctypes.c_int
         lib.nep_device_arch.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
         lib.nep_device_arch.restype = ctypes.c_int
+        i64 = ctypes.c_int64
+        lib.nep_fold_split_workspace_bytes.argtypes = [i64, i64]
+        lib.nep_fold_split_workspace_bytes.restype = ctypes.c_size_t
+        lib.nep_fold_split.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p,
+                                       ctypes.c_void_p, i64, i64, i64, i64, i64, i64, u32, u32,
+                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.nep_fold_split.restype = ctypes.c_int
         if lib.nep_abi_version() != 2:
             raise RuntimeError("libneptune_hip ABI version mismatch; rebuild the library")
         _lib = lib

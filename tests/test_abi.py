@@ -67,3 +67,27 @@ def test_argument_checks_need_no_gpu():
     out = ctypes.c_uint64()
     assert lib.nep_get_kernel(0, b"k", ctypes.byref(out)) == 1
     assert lib.nep_compile(None, b"x", b"", None, ctypes.byref(out)) == 1
+
+
+def test_split_entry_point_checks_its_arguments_before_any_launch():
+    """nep_fold_split refuses inconsistent shapes (no GPU is touched before the checks)."""
+    lib = hip.load_library()
+    ws = ctypes.c_void_p(16)
+    common = dict(x=ctypes.c_void_p(16), out=ctypes.c_void_p(16))
+
+    def call(partial=1, merge=1, rows=4, ncols=3000, nparts=3, block=1024, threads=256, ppw=4,
+             workspace=ws, nbytes=1 << 20):
+        return lib.nep_fold_split(partial, merge, common["x"], common["out"], rows, ncols, ncols, 1,
+                                  nparts, block, threads, ppw, workspace, nbytes, None)
+
+    assert lib.nep_fold_split_workspace_bytes(64, 256) == 16 * 64 * 256
+    assert lib.nep_fold_split_workspace_bytes(0, 256) == 0
+    for kwargs, needle in (({"partial": 0}, b"null kernel"), ({"nparts": 2}, b"ceil(ncols / block)"),
+                           ({"block": 1000, "nparts": 3}, b"power of two"),
+                           ({"ncols": 5000 * 1024, "nparts": 5000}, b"capacity"),
+                           ({"threads": 100}, b"multiple of 64"), ({"ppw": 0}, b"parts_per_workgroup"),
+                           ({"nbytes": 100}, b"workspace holds 100 bytes"),
+                           ({"workspace": None}, b"workspace")):
+        assert call(**kwargs) == 1, kwargs
+        assert needle in lib.nep_last_error(), (kwargs, lib.nep_last_error())
+    assert call(rows=0) == 0            # nothing to do, nothing launched
