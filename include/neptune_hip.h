@@ -133,6 +133,24 @@ int nep_fold_split(uint64_t partial_kernel, uint64_t merge_kernel, const void* x
                    uint32_t parts_per_workgroup, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+/*
+ * nep_fold_split without allocation, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Same arguments and results as nep_fold_split minus the workspace: the scratch is
+ * a fixed device array inside this library, one per GPU, of nep_fold_split_noalloc_capacity()
+ * bytes (8 MiB: rows * nparts <= 524288).  Larger requests fail with NEP_ERR_INVALID before
+ * any launch.  Calls no hipMalloc/hipFree.  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race and must be serialised
+ * by the caller.
+ */
+int nep_fold_split_noalloc(uint64_t partial_kernel, uint64_t merge_kernel, const void* x,
+                           void* out, int64_t rows, int64_t ncols, int64_t row_stride,
+                           int64_t col_stride, int64_t nparts, int64_t block,
+                           uint32_t partial_threads, uint32_t parts_per_workgroup, void* stream);
+
+/* Bytes of the per-GPU scratch array nep_fold_split_noalloc uses. */
+size_t nep_fold_split_noalloc_capacity(void);
+
 /* Name of the current device's ISA (e.g. "gfx950:sramecc+:xnack-") into buf. */
 int nep_device_arch(char* buf, size_t buf_len);
 

@@ -375,3 +375,67 @@ int nep_fold_split(uint64_t partial_kernel, uint64_t merge_kernel, const void* x
 
 }  // extern "C"
 
+// ---------------------------------------------------------------- split plan without allocation
+// nep_fold_split_noalloc's scratch: a file-scope device array, one copy per GPU the library
+// runs on, held until the process ends.  In host code `scratch` names a host-side stand-in
+// symbol, not device memory: every host use goes through the per-device address that
+// hipGetSymbolAddress returns (kept in g_scratch_address).  Every call on a GPU shares that
+// GPU's copy and overwrites it; calls that overlap on one GPU race.  The split writes every
+// partial before the merge reads it, so nothing has to start at zero.
+namespace {
+
+constexpr size_t kSplitScratchBytes = size_t(8) << 20;   // 524288 partials of 16 bytes
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kSplitScratchBytes];
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device with it current.
+int scratch_address(void** out) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+  if (device < 0 || device >= kMaxDevices)
+    return fail(NEP_ERR_INVALID, "nep_fold_split_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[device] == nullptr) {
+    void* address = nullptr;
+    err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress(scratch)");
+    if (address == nullptr)
+      return fail(NEP_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_address[device] = address;
+  }
+  *out = g_scratch_address[device];
+  return NEP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t nep_fold_split_noalloc_capacity(void) { return kSplitScratchBytes; }
+
+int nep_fold_split_noalloc(uint64_t partial_kernel, uint64_t merge_kernel, const void* x,
+                           void* out, int64_t rows, int64_t ncols, int64_t row_stride,
+                           int64_t col_stride, int64_t nparts, int64_t block,
+                           uint32_t partial_threads, uint32_t parts_per_workgroup, void* stream) {
+  int rc = check_split("nep_fold_split_noalloc", partial_kernel, merge_kernel, x, out, rows, ncols,
+                       nparts, block, partial_threads, parts_per_workgroup);
+  if (rc != NEP_OK) return rc;
+  const size_t need = nep_fold_split_workspace_bytes(rows, nparts);
+  if (need > kSplitScratchBytes)
+    return fail(NEP_ERR_INVALID,
+                "nep_fold_split_noalloc: " + std::to_string(rows) + " rows x " +
+                    std::to_string(nparts) + " partials need " + std::to_string(need) +
+                    " bytes of scratch, more than the " + std::to_string(kSplitScratchBytes) +
+                    " bytes this library holds per GPU; call nep_fold_split with a workspace");
+  if (rows == 0) return NEP_OK;
+  void* base = nullptr;
+  rc = scratch_address(&base);
+  if (rc != NEP_OK) return rc;
+  return run_split(partial_kernel, merge_kernel, x, out, rows, ncols, row_stride, col_stride,
+                   nparts, block, partial_threads, parts_per_workgroup, base, stream);
+}
+
+}  // extern "C"

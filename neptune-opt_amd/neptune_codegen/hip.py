@@ -20,7 +20,8 @@ CACHE_DIR = PACKAGE_DIR / "_codeobj"
 NEP_OK = 0
 EXPORTED = ("nep_abi_version", "nep_last_error", "nep_compile", "nep_compile_code_object",
             "nep_free", "nep_module_load", "nep_get_kernel", "nep_launch", "nep_launch_packed",
-            "nep_device_arch", "nep_fold_split_workspace_bytes", "nep_fold_split")
+            "nep_device_arch", "nep_fold_split_workspace_bytes", "nep_fold_split",
+            "nep_fold_split_noalloc", "nep_fold_split_noalloc_capacity")
 
 _lock = threading.Lock()
 _lib = None
@@ -79,6 +80,12 @@ def load_library(require_torch: bool = True) -> ctypes.CDLL:
                                        ctypes.c_void_p, i64, i64, i64, i64, i64, i64, u32, u32,
                                        ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.nep_fold_split.restype = ctypes.c_int
+        lib.nep_fold_split_noalloc.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p,
+                                               ctypes.c_void_p, i64, i64, i64, i64, i64, i64, u32,
+                                               u32, ctypes.c_void_p]
+        lib.nep_fold_split_noalloc.restype = ctypes.c_int
+        lib.nep_fold_split_noalloc_capacity.argtypes = []
+        lib.nep_fold_split_noalloc_capacity.restype = ctypes.c_size_t
         if lib.nep_abi_version() != 2:
             raise RuntimeError("libneptune_hip ABI version mismatch; rebuild the library")
         _lib = lib
