@@ -11,9 +11,10 @@
 //    per tile.  Tiles whose largest |v| reaches 2^15 are stored as v * 2^-e (exact: bf16
 //    values keep their 8 significant bits in fp16 down to |v| >= 2^(e-17)); the fold feeds
 //    such a tile P * 2^e instead of P and weights its row sum by 2^-e, both exact, so no
-//    accumulator is rescaled.  e is capped at 24: |v| >= 2^39 overflows fp16 and yields
-//    inf/NaN rows.  The image is written once per call and read by every query block of the
-//    head.
+//    accumulator is rescaled.  A tile value below 2^(e-14) keeps an absolute precision of
+//    2^(e-25) only, so the caller bounds e (e_max); a tile above it, or holding inf/NaN,
+//    clears *status, which the caller turns into an error.  The image is written once per
+//    call and read by every query block of the head.
 //  * attention_fwd: one workgroup = 8 wave64s = BLOCK_M = 256 queries (32 per wave), one
 //    workgroup per CU (two waves per SIMD): each staged K / V^T tile serves 256 queries.
 //    K (bf16, the caller's strided rows, bounds-checked buffer loads) and the V^T image go
@@ -90,6 +91,7 @@ __device__ __forceinline__ int swizzle(int row) {
 template <int D>
 __device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
                                                   u16* __restrict__ vt, int* __restrict__ exps,
+                                                  int* __restrict__ status, int e_max,
                                                   int heads, int sk, i64 vsb, i64 vsh, i64 vss) {
   constexpr int CH = D / 8;                         // 16-byte chunks per key row
   constexpr int UNITS = (kAttnBN / 2) * CH;         // (key pair, dim chunk) units
@@ -129,8 +131,10 @@ __device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
   if ((tid & 63) == 0) wave_max[tid >> 6] = mx;
   __syncthreads();
   mx = max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]));
-  const u32 ebits = mx >> 7;
-  const int e = ebits >= kVtScaleFrom ? min((int)(ebits - kVtScaleFrom + 1), 24) : 0;
+  const u32 ebits = mx >> 7;                  // 255: the tile holds inf or NaN
+  const int e_tile = ebits >= kVtScaleFrom ? (int)(ebits - kVtScaleFrom + 1) : 0;
+  // the fold's scaling arithmetic covers e <= 24; a refused tile is clamped into it
+  const int e = min(e_tile, 24);
   const float down = exp2_int(-e);
 
 #pragma unroll
@@ -153,7 +157,10 @@ __device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
 #pragma unroll
   for (int c = tid; c < D * kAttnBN / 8; c += kAttnThreads)
     store16(dst + c * 8, *(const u32x4*)(img + c * 8));
-  if (tid == 0) exps[bh * ntiles + t] = e;
+  if (tid == 0) {
+    exps[bh * ntiles + t] = e;
+    if (e_tile > e_max) *status = 0;
+  }
 }
 
 // LDS-DMA of one tile operand: 16 bytes per lane into 1 KB blocks; piece i of wave w fills

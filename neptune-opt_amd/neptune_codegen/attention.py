@@ -27,6 +27,14 @@ LOG2E = 1.4426950408889634
 BLOCK_M = 256           # queries per fold workgroup (8 waves of 32)
 BLOCK_N = 64            # keys per tile (one V^T image per tile)
 K_ROW_STRIDE_MAX = 1 << 24   # K rows are addressed with 32-bit byte offsets within a tile
+# V^T tiles are fp16 images of v * 2^-e, e the tile's exponent (0 below 2^15).  A tile value
+# below 2^(e - 14) keeps only an absolute precision of 2^(e - 25), which bounds the error it
+# adds to O; e <= 13 keeps that under 2^-12, a quarter of the bf16 absolute tolerance.  Larger
+# tiles, and inf/NaN, are refused.  (fp32 accumulation of O, |O acc| <= keys * 2^8 * 2^28,
+# cannot overflow at this bound.)
+V_EXPONENT_MAX = 13
+V_RANGE_MESSAGE = ("attention fold: V must be finite with |v| < 2^28 (a larger value would take "
+                   "the fp16 precision of the other values of its 64-key tile)")
 
 
 def _program(head_dim: int, causal: bool) -> hip.Program:
@@ -70,7 +78,22 @@ def _kernel_ready(t):
 
 def run_attention(q, k, v, *, scale: float | None = None, causal: bool = True,
                   return_lse: bool = False):
-    """Attention fold on the current stream; see the module docstring for the contract."""
+    """Attention fold on the current stream; see the module docstring for the contract.  V
+    holding inf/NaN or |v| >= 2^28 is refused by a device-side assert (V_RANGE_MESSAGE),
+    raised at the next synchronisation."""
+    import torch
+
+    out, lse, status = launch_attention(q, k, v, scale=scale, causal=causal, return_lse=return_lse)
+    if status is not None:
+        torch._assert_async(status, V_RANGE_MESSAGE)
+    return (out, lse) if return_lse else out
+
+
+def launch_attention(q, k, v, *, scale: float | None = None, causal: bool = True,
+                     return_lse: bool = False):
+    """(out, lse or None, status or None): the fold's launches without the range assert.
+    `status` is one int32 on the device, 1 when every V tile was in range and 0 otherwise
+    (None when nothing was launched)."""
     import torch
     from torch._subclasses.fake_tensor import FakeTensor
 
@@ -80,7 +103,7 @@ def run_attention(q, k, v, *, scale: float | None = None, causal: bool = True,
     out = torch.empty(shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device) if return_lse else None
     if metadata or out.numel() == 0:
-        return (out, lse) if return_lse else out
+        return out, lse, None
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     if not math.isfinite(scale) or scale <= 0:
         raise ValueError("attention scale must be finite and positive")
@@ -95,21 +118,23 @@ def run_attention(q, k, v, *, scale: float | None = None, causal: bool = True,
     exps = torch.empty((B * H * ntiles,), dtype=torch.int32, device=q.device)
     prog = _program(D, causal)
     pack = prog.kernel(attention_pack_kernel_name(D),
-                       (hip.PTR,) * 3 + (hip.I32,) * 2 + (hip.I64,) * 3, 256, device)
+                       (hip.PTR,) * 4 + (hip.I32,) * 3 + (hip.I64,) * 3, 256, device)
     fold = prog.kernel(attention_kernel_name(D, causal),
                        (hip.PTR,) * 6 + (hip.I32,) * 3 + (hip.I64,) * 6 + (hip.F32,),
                        ATTN_FOLD_THREADS, device)
     stream = hip.current_stream(q.device)
+    # one status word: set here, cleared by the pack kernel for a V tile out of range
+    status = torch.ones(1, dtype=torch.int32, device=q.device)
     pack.launch((B * H * ntiles,),
-                (v.data_ptr(), vt.data_ptr(), exps.data_ptr(), H, Sk, v.stride(0), v.stride(1),
-                 v.stride(2)), stream)
+                (v.data_ptr(), vt.data_ptr(), exps.data_ptr(), status.data_ptr(),
+                 V_EXPONENT_MAX, H, Sk, v.stride(0), v.stride(1), v.stride(2)), stream)
     nqb = (Sq + BLOCK_M - 1) // BLOCK_M
     fold.launch((nqb * B * H,),
                 (q.data_ptr(), k.data_ptr(), vt.data_ptr(), exps.data_ptr(), out.data_ptr(),
                  lse.data_ptr() if lse is not None else 0, H, Sq, Sk,
                  q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
                  scale * LOG2E), stream)
-    return (out, lse) if return_lse else out
+    return out, lse, status
 
 
 attention_fold = run_attention

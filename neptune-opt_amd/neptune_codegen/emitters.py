@@ -528,9 +528,9 @@ def emit_attention_source(head_dim: int, causal: bool, waves_per_eu: int | None 
         "Q K^T, fp16 MFMA for P V, fp32 running max/sum.\n",
         kernel_header("nep_device.h", "nep_attention.h"),
         f'extern "C" __global__ void __launch_bounds__(256) {pack}(const void* v, void* vt, int* exps, '
-        "int heads, int sk, long long vsb, long long vsh, long long vss) {\n"
-        f"  nep::attention_vt_pack<{head_dim}>((const __bf16*)v, (nep::u16*)vt, exps, heads, sk, vsb, "
-        "vsh, vss);\n}\n",
+        "int* status, int e_max, int heads, int sk, long long vsb, long long vsh, long long vss) {\n"
+        f"  nep::attention_vt_pack<{head_dim}>((const __bf16*)v, (nep::u16*)vt, exps, status, e_max, "
+        "heads, sk, vsb, vsh, vss);\n}\n",
         f'extern "C" __global__ void __launch_bounds__({ATTN_FOLD_THREADS}, {wpe}) {name}(const void* q, const void* k, '
         "const void* vt, const int* exps, void* o, float* lse, int heads, int sq, int sk, "
         "long long qsb, long long qsh, long long qss, long long ksb, long long ksh, long long kss, "

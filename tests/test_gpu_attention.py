@@ -105,6 +105,46 @@ def test_attention_large_values_use_scaled_tiles(causal):
     torch.testing.assert_close(got.cpu().float(), want.float(), rtol=1.6e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_largest_accepted_v_tile_next_to_masked_and_normal_keys(causal):
+    """Tiles holding |v| just below 2^28 (tile exponent 13, the largest accepted): packed as
+    v * 2^-13, fed P * 2^13 with a row-sum weight of 2^-13, the reference max held 6 higher.
+    The tile's other values keep 2^-12 absolute precision -- also on causal rows that see the
+    tile but not its large key (queries 64-99 for the key at 100) -- and later tiles' P stay
+    within fp16's normal range down to 2^-8 of their unlifted value."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(13)
+    B, H, S, D = 1, 1, 400, 128
+    q = torch.randn(B, H, S, D, generator=g).bfloat16()
+    k = torch.randn(B, H, S, D, generator=g).bfloat16()
+    v = torch.randn(B, H, S, D, generator=g)
+    v[0, 0, 100, 3] = 2.0 ** 27 * 1.9921875          # largest bf16 below 2^28
+    v[0, 0, 5, 9] = -2.0 ** 27                        # tile 0, another exponent-13 tile
+    v = v.bfloat16()
+    _say(f"attention exponent-13 V tiles causal={causal}")
+    out, lse, status = CG.launch_attention(q.to(dev), k.to(dev), v.to(dev), causal=causal)
+    assert status.item() == 1
+    want = R.attention_reference(q, k, v, causal=causal).float()
+    got = out.cpu().float()
+    assert torch.isfinite(got).all()
+    torch.testing.assert_close(got, want, rtol=1.6e-2, atol=1e-3)
+
+
+def test_attention_refuses_v_out_of_range_through_its_status_word():
+    """|v| >= 2^28 or inf/NaN in V clear the status word that run_attention asserts on (read
+    back here instead, so no device-side assert fires); in-range inputs leave it set."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(14)
+    q, k, v = (torch.randn(1, 2, 200, 64, generator=g).bfloat16() for _ in range(3))
+    for value, expected in ((2.0 ** 27, 1), (2.0 ** 28, 0), (2.0 ** 40, 0), (float("inf"), 0),
+                            (float("nan"), 0), (-(2.0 ** 100), 0)):
+        bad = v.clone()
+        bad[0, 1, 150, 7] = value
+        _say(f"attention V range status, v={value}")
+        _, _, status = CG.launch_attention(q.to(dev), k.to(dev), bad.to(dev), causal=True)
+        assert status.item() == expected, value
+
+
 def test_attention_strided_layout_and_scale():
     """[B, S, H, D] storage viewed as [B, H, S, D] (the common projection layout)."""
     dev = _dev()
