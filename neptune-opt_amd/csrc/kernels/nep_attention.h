@@ -163,6 +163,85 @@ __device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
   }
 }
 
+// 32-bit LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ u32 lds_address(const void* p) {
+  return (u32)(unsigned long long)(const __attribute__((address_space(3))) void*)p;
+}
+
+// S^T = K Q^T of one 64-key tile at head dim 128 (both 32-key blocks, 16 MFMAs) as one
+// instruction block.  The compiler, left to itself, waits for each LDS read right before its
+// MFMA, which serialises the phase on LDS latency; here the K fragments are read ahead into
+// v224-v255 (eight quads, reserved through the clobber list) and each MFMA waits only for its
+// own read: LDS reads retire in order, so lgkmcnt counts down.  A quad is refilled one MFMA
+// after the MFMA that read it.  The block starts with lgkmcnt(0), so no earlier scalar load
+// (also counted by lgkmcnt, retiring out of order) can be outstanding, and ends with s_nops
+// for the wait states before VALU reads the last MFMA's result.  addr[s] is the LDS address
+// of the k-step s fragment of key block 0; block 1 is 32 rows (8192 bytes) further.
+__device__ __forceinline__ void attention_s_tile_d128(const u32 (&addr)[8], const bf16x8 (&q)[8],
+                                                      f32x16& s0, f32x16& s1) {
+  asm volatile(
+      "s_waitcnt lgkmcnt(0)\n"
+      "ds_read_b128 v[224:227], %[a0]\n"
+      "ds_read_b128 v[228:231], %[a1]\n"
+      "ds_read_b128 v[232:235], %[a2]\n"
+      "ds_read_b128 v[236:239], %[a3]\n"
+      "ds_read_b128 v[240:243], %[a4]\n"
+      "ds_read_b128 v[244:247], %[a5]\n"
+      "ds_read_b128 v[248:251], %[a6]\n"
+      "ds_read_b128 v[252:255], %[a7]\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s0], v[224:227], %[q0], 0\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s0], v[228:231], %[q1], %[s0]\n"
+      "ds_read_b128 v[224:227], %[a0] offset:8192\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s0], v[232:235], %[q2], %[s0]\n"
+      "ds_read_b128 v[228:231], %[a1] offset:8192\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s0], v[236:239], %[q3], %[s0]\n"
+      "ds_read_b128 v[232:235], %[a2] offset:8192\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s0], v[240:243], %[q4], %[s0]\n"
+      "ds_read_b128 v[236:239], %[a3] offset:8192\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s0], v[244:247], %[q5], %[s0]\n"
+      "ds_read_b128 v[240:243], %[a4] offset:8192\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s0], v[248:251], %[q6], %[s0]\n"
+      "ds_read_b128 v[244:247], %[a5] offset:8192\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s0], v[252:255], %[q7], %[s0]\n"
+      "ds_read_b128 v[248:251], %[a6] offset:8192\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s1], v[224:227], %[q0], 0\n"
+      "ds_read_b128 v[252:255], %[a7] offset:8192\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s1], v[228:231], %[q1], %[s1]\n"
+      "s_waitcnt lgkmcnt(5)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s1], v[232:235], %[q2], %[s1]\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s1], v[236:239], %[q3], %[s1]\n"
+      "s_waitcnt lgkmcnt(3)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s1], v[240:243], %[q4], %[s1]\n"
+      "s_waitcnt lgkmcnt(2)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s1], v[244:247], %[q5], %[s1]\n"
+      "s_waitcnt lgkmcnt(1)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s1], v[248:251], %[q6], %[s1]\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      "v_mfma_f32_32x32x16_bf16 %[s1], v[252:255], %[q7], %[s1]\n"
+      "s_nop 7\n"
+      "s_nop 7\n"
+      "s_nop 7\n"
+      : [s0] "=&v"(s0), [s1] "=&v"(s1)
+      : [a0] "v"(addr[0]), [a1] "v"(addr[1]), [a2] "v"(addr[2]), [a3] "v"(addr[3]),
+        [a4] "v"(addr[4]), [a5] "v"(addr[5]), [a6] "v"(addr[6]), [a7] "v"(addr[7]),
+        [q0] "v"(q[0]), [q1] "v"(q[1]), [q2] "v"(q[2]), [q3] "v"(q[3]), [q4] "v"(q[4]),
+        [q5] "v"(q[5]), [q6] "v"(q[6]), [q7] "v"(q[7])
+      : "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234",
+        "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245",
+        "v246", "v247", "v248", "v249", "v250", "v251", "v252", "v253", "v254", "v255", "memory");
+}
+
 // LDS-DMA of one tile operand: 16 bytes per lane into 1 KB blocks; piece i of wave w fills
 // block i*W + w (W waves per workgroup).  `dst` is the wave's block (wave-uniform, it becomes M0).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* dst, int voffset,
@@ -261,16 +340,25 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
   auto body = [&](int tile, const unsigned char* kt, const unsigned char* vtt, int e) {
     const int k0 = tile * kAttnBN;
     if (CAUSAL && k0 > qw + 31) return;   // tile entirely above this wave's diagonal
-    // ---- S^T = K Q^T for the two 32-key blocks of the tile
+    // ---- S^T = K Q^T for the two 32-key blocks of the tile (head dim 128: one instruction
+    // block with the K reads ahead of their MFMAs)
     f32x16 sacc[2];
+    if constexpr (D == 128) {
+      const u32 krow0 = lds_address(kt) + l32 * (CH * 16);
+      u32 addr[8];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sacc[kb] = f32x16{};
-      const unsigned char* krow = kt + (kb * 32 + l32) * (CH * 16);
+      for (int s = 0; s < 8; ++s) addr[s] = krow0 + (((2 * s + hi) ^ ksw) << 4);
+      attention_s_tile_d128(addr, qreg, sacc[0], sacc[1]);
+    } else {
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        const bf16x8 a = *(const bf16x8*)(krow + (((2 * s + hi) ^ ksw) << 4));
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[kb], 0, 0, 0);
+      for (int kb = 0; kb < 2; ++kb) {
+        sacc[kb] = f32x16{};
+        const unsigned char* krow = kt + (kb * 32 + l32) * (CH * 16);
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+          const bf16x8 a = *(const bf16x8*)(krow + (((2 * s + hi) ^ ksw) << 4));
+          sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[kb], 0, 0, 0);
+        }
       }
     }
     // ---- masks only on the diagonal tile and the ragged last tile
