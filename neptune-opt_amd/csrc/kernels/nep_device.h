@@ -86,12 +86,16 @@ __device__ __forceinline__ u32 bf16x2_rne(float a, float b) {
 struct F32 {
   typedef float T;
   static constexpr int kVec = 4;  // elements per 16-byte load
+  static constexpr u32 kNegInfWord = 0xff800000u;  // a 32-bit word of -inf elements
   __device__ static __forceinline__ float load(const T* p) { return *p; }
   __device__ static __forceinline__ void store(T* p, float v) { *p = v; }
   __device__ static __forceinline__ float round(float v) { return v; }
   __device__ static __forceinline__ void unpack(const u32x4& w, float* o) {
     o[0] = as_f32(w.x); o[1] = as_f32(w.y); o[2] = as_f32(w.z); o[3] = as_f32(w.w);
   }
+  // unpack for a word unpacked again later: the values are not kept between the two (for
+  // fp32 the word is the values, so this is unpack).
+  __device__ static __forceinline__ void reunpack(const u32x4& w, float* o) { unpack(w, o); }
   __device__ static __forceinline__ u32x4 pack(const float* v) {
     u32x4 w; w.x = as_u32(v[0]); w.y = as_u32(v[1]); w.z = as_u32(v[2]); w.w = as_u32(v[3]);
     return w;
@@ -101,6 +105,7 @@ struct F32 {
 struct BF16 {
   typedef u16 T;
   static constexpr int kVec = 8;
+  static constexpr u32 kNegInfWord = 0xff80ff80u;
   __device__ static __forceinline__ float load(const T* p) { return bf16_bits_to_f32(*p); }
   __device__ static __forceinline__ void store(T* p, float v) { *p = (u16)bf16x2_rne(v, v); }
   __device__ static __forceinline__ float round(float v) { return as_f32(bf16x2_rne(v, v) << 16); }
@@ -109,6 +114,14 @@ struct BF16 {
     o[2] = as_f32(w.y << 16); o[3] = as_f32(w.y & 0xffff0000u);
     o[4] = as_f32(w.z << 16); o[5] = as_f32(w.z & 0xffff0000u);
     o[6] = as_f32(w.w << 16); o[7] = as_f32(w.w & 0xffff0000u);
+  }
+  // unpack whose results the compiler cannot share with another unpack of the same word
+  // (through an opaque copy of the word), so a caller that unpacks a held row once per pass
+  // holds 16-bit words, not fp32 values.
+  __device__ static __forceinline__ void reunpack(const u32x4& w, float* o) {
+    u32x4 c = w;
+    asm volatile("" : "+v"(c));
+    unpack(c, o);
   }
   __device__ static __forceinline__ u32x4 pack(const float* v) {
     u32x4 w;
@@ -125,6 +138,7 @@ struct BF16 {
 struct F16 {
   typedef _Float16 T;
   static constexpr int kVec = 8;
+  static constexpr u32 kNegInfWord = 0xfc00fc00u;
   __device__ static __forceinline__ float load(const T* p) { return (float)*p; }
   __device__ static __forceinline__ void store(T* p, float v) { *p = (_Float16)v; }
   __device__ static __forceinline__ float round(float v) { return (float)(_Float16)v; }
@@ -132,6 +146,11 @@ struct F16 {
     const half2_t h0 = as_half2(w.x), h1 = as_half2(w.y), h2 = as_half2(w.z), h3 = as_half2(w.w);
     o[0] = (float)h0.x; o[1] = (float)h0.y; o[2] = (float)h1.x; o[3] = (float)h1.y;
     o[4] = (float)h2.x; o[5] = (float)h2.y; o[6] = (float)h3.x; o[7] = (float)h3.y;
+  }
+  __device__ static __forceinline__ void reunpack(const u32x4& w, float* o) {
+    u32x4 c = w;
+    asm volatile("" : "+v"(c));
+    unpack(c, o);
   }
   __device__ static __forceinline__ u32x4 pack(const float* v) {
     half2_t h0, h1, h2, h3;

@@ -138,9 +138,52 @@ struct RowComm {
 };
 
 // ---------------------------------------------------------------- exact path
-// The reference chunk (emitters.py:459-488) over one thread's slots of one tile, merged into
-// the running state.  Used by every non-exponential fold and, for exponential folds, only on
-// rows whose fast path met NaN or +inf.
+// The reference chunk of an exponential fold (emitters.py:459-488) over one lane's UNROLL
+// slots of VEC values.  slot(u, v) fills v[0..VEC) with slot u's values and returns whether
+// the slot lies in the row; it is called once per pass, so a caller may hand out values it
+// recomputes rather than holds.
+template <class F, int UNROLL, int VEC, class Slot>
+__device__ __forceinline__ State log_chunk(Slot slot, float n) {
+  State c;
+  int status = 0, seen = 0;
+  float m = -kInf;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    float v[VEC];
+    if (!slot(u, v)) continue;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float p = F::phi(v[j], n);
+      if (is_nan(p)) status |= 1;
+      if (p == kInf) status |= 2;
+      if (is_finite(p)) {
+        seen = 1;
+        m = __builtin_fmaxf(m, p);
+      }
+    }
+  }
+  const float den = seen ? m : 0.0f;
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    float v[VEC];
+    if (!slot(u, v)) continue;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float p = F::phi(v[j], n);
+      if (is_finite(p)) acc += fast_exp(p - den);
+    }
+  }
+  c.m = m;
+  c.acc = acc;
+  c.seen = seen;
+  c.status = status;
+  return c;
+}
+
+// The reference chunk over one thread's slots of one tile, merged into the running state.
+// Used by every non-exponential fold and, for exponential folds, only on rows whose fast path
+// met NaN or +inf.
 template <class F, class St, int TPR, int UNROLL, bool VECTOR>
 __device__ __forceinline__ void exact_tile(State& s, const typename St::T* row, i64 stride_col,
                                            i64 tile, i64 c1, int t, float n) {
@@ -150,39 +193,12 @@ __device__ __forceinline__ void exact_tile(State& s, const typename St::T* row, 
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) ok[u] = TL::load_slot(row, stride_col, tile, c1, t, u, v);
   if constexpr (F::kLog) {
-    State c;
-    int status = 0, seen = 0;
-    float m = -kInf;
+    auto slot = [&](int u, float* w) {
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      if (!ok[u]) continue;
-#pragma unroll
-      for (int j = 0; j < TL::VEC; ++j) {
-        const float p = F::phi(v[u * TL::VEC + j], n);
-        if (is_nan(p)) status |= 1;
-        if (p == kInf) status |= 2;
-        if (is_finite(p)) {
-          seen = 1;
-          m = __builtin_fmaxf(m, p);
-        }
-      }
-    }
-    const float den = seen ? m : 0.0f;
-    float acc = 0.0f;
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      if (!ok[u]) continue;
-#pragma unroll
-      for (int j = 0; j < TL::VEC; ++j) {
-        const float p = F::phi(v[u * TL::VEC + j], n);
-        if (is_finite(p)) acc += fast_exp(p - den);
-      }
-    }
-    c.m = m;
-    c.acc = acc;
-    c.seen = seen;
-    c.status = status;
-    s = merge_state<F>(s, c);
+      for (int j = 0; j < TL::VEC; ++j) w[j] = v[u * TL::VEC + j];
+      return ok[u];
+    };
+    s = merge_state<F>(s, log_chunk<F, UNROLL, TL::VEC>(slot, n));
   } else {
     // Streaming update (one repair per tile instead of merge_state's two): the tile's terms
     // are taken at the combined producer value, and only the carried accumulator is
@@ -227,20 +243,10 @@ __device__ __forceinline__ void exact_tile(State& s, const typename St::T* row, 
   }
 }
 
-// Exact state of the columns [c0, c1) of one row, complete in every lane of the row.
-template <class F, class St, int TPR, int UNROLL, bool VECTOR>
-__device__ __forceinline__ State exact_row_state(const typename St::T* row, i64 stride_col,
-                                                 i64 c0, i64 c1, int t, float n,
-                                                 State* lds_state) {
-  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+// A row's lane states merged (lanes in order, then waves in order), complete in every lane.
+template <class F, int TPR>
+__device__ __forceinline__ State row_state(State s, State* lds_state) {
   typedef RowComm<TPR> RC;
-  State s;
-  s.m = 0.0f;
-  s.acc = consumer_init<F>();
-  s.seen = 0;
-  s.status = 0;
-  for (i64 tile = c0; tile < c1; tile += TL::TILE)
-    exact_tile<F, St, TPR, UNROLL, VECTOR>(s, row, stride_col, tile, c1, t, n);
   s = group_merge<F, RC::G>(s);
   if constexpr (RC::WPR > 1) {
     const int wave = threadIdx.x >> 6, first = (wave / RC::WPR) * RC::WPR;
@@ -253,6 +259,28 @@ __device__ __forceinline__ State exact_row_state(const typename St::T* row, i64 
     s = r;
   }
   return s;
+}
+
+template <class F>
+__device__ __forceinline__ State empty_state() {
+  State s;
+  s.m = 0.0f;
+  s.acc = consumer_init<F>();
+  s.seen = 0;
+  s.status = 0;
+  return s;
+}
+
+// Exact state of the columns [c0, c1) of one row, complete in every lane of the row.
+template <class F, class St, int TPR, int UNROLL, bool VECTOR>
+__device__ __forceinline__ State exact_row_state(const typename St::T* row, i64 stride_col,
+                                                 i64 c0, i64 c1, int t, float n,
+                                                 State* lds_state) {
+  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+  State s = empty_state<F>();
+  for (i64 tile = c0; tile < c1; tile += TL::TILE)
+    exact_tile<F, St, TPR, UNROLL, VECTOR>(s, row, stride_col, tile, c1, t, n);
+  return row_state<F, TPR>(s, lds_state);
 }
 
 // Final value of a row from its exact state (emitters.py:522-532 for exponential folds).
@@ -269,7 +297,9 @@ __device__ __forceinline__ float finalize_state(const State& s, float n) {
 }
 
 // ---------------------------------------------------------------- fast exponential path
-// Raw slots of one tile: 16-byte words (VECTOR) or one element each (strided path).
+// Raw slots of one tile: 16-byte words (VECTOR) or one element each (strided path).  Slots
+// past the row's end hold -inf elements, so a fold whose phi is the identity needs no per-element
+// test of `ok` (-inf neither raises a max nor adds to an exponential sum).
 template <class St, int UNROLL, bool VECTOR>
 struct RawTile {
   u32x4 w[VECTOR ? UNROLL : 1];
@@ -287,9 +317,11 @@ __device__ __forceinline__ void load_raw(RawTile<St, UNROLL, VECTOR>& r,
     const i64 e = tile + (i64)(u * TPR + t) * TL::VEC;
     r.ok[u] = e < c1;
     if constexpr (VECTOR) {
-      if (r.ok[u]) r.w[u] = load16(row + e);
+      // a uniform base plus a 32-bit lane offset (the tile is below 2^31 elements)
+      const u32 f = St::kNegInfWord;
+      r.w[u] = r.ok[u] ? load16(row + tile + (u32)((u * TPR + t) * TL::VEC)) : u32x4{f, f, f, f};
     } else {
-      if (r.ok[u]) r.s[u] = St::load(row + e * stride_col);
+      r.s[u] = r.ok[u] ? St::load(row + e * stride_col) : -kInf;
     }
   }
 }
@@ -304,38 +336,70 @@ __device__ __forceinline__ void load_raw(RawTile<St, UNROLL, VECTOR>& r,
 // row maximum contributes exactly 1 (one more VALU op per element).  The readout uses it, so
 // that a log-probability of 0 comes out as 0 rather than as the rounding residue of m*log2e.
 // Fold one raw tile into a lane's exponential state.
-template <class F, class St, int TPR, int UNROLL, bool VECTOR, bool CENTERED>
-__device__ __forceinline__ void log_fold_tile(LogLane& s,
-                                              const RawTile<St, UNROLL, VECTOR>& cur, float n) {
-  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
-  float p[TL::K];
-  float tm = -kInf;
+//
+// The held words of a raw tile, made opaque to the compiler: unpacks after this point cannot
+// reuse values unpacked before it, so a pass over a held row re-derives its fp32 values from
+// the 16-bit words instead of keeping them live (no instruction is emitted).
+template <class St, int UNROLL, bool VECTOR>
+__device__ __forceinline__ void reopen(RawTile<St, UNROLL, VECTOR>& r) {
+  if constexpr (VECTOR) {
 #pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
+    for (int u = 0; u < UNROLL; ++u) asm volatile("" : "+v"(r.w[u]));
+  }
+}
+
+// The centred (readout) fold holds a whole row per lane group and keeps the raw words for the
+// readout, so it recomputes phi from them in each pass rather than holding the K fp32 terms
+// across the max (K = 64 for a 16-bit row of 8 slots: 64 VGPRs, which would cut the readout
+// to one 8-wave workgroup per CU).  The terms and their order are the same, so results are
+// unchanged.
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, bool CENTERED>
+__device__ __forceinline__ void log_fold_tile(LogLane& s, RawTile<St, UNROLL, VECTOR>& cur,
+                                              float n) {
+  typedef Tiles<St, TPR, UNROLL, VECTOR> TL;
+  auto terms = [&](int u, float* p) {
     float v[TL::VEC];
     if constexpr (VECTOR) St::unpack(cur.w[u], v);
     else v[0] = cur.s[u];
 #pragma unroll
     for (int j = 0; j < TL::VEC; ++j) {
-      const int k = u * TL::VEC + j;
-      p[k] = cur.ok[u] ? F::phi(v[j], n) : -kInf;
-      tm = __builtin_fmaxf(tm, p[k]);
+      if constexpr (F::kPhiIdentity) p[j] = v[j];
+      else p[j] = cur.ok[u] ? F::phi(v[j], n) : -kInf;
     }
+  };
+  float tm = -kInf;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    float p[TL::VEC];
+    terms(u, p);
+#pragma unroll
+    for (int j = 0; j < TL::VEC; ++j) tm = __builtin_fmaxf(tm, p[j]);
   }
+  if constexpr (CENTERED) reopen(cur);
   const float mn = __builtin_fmaxf(s.m, tm);
   if (mn == -kInf) {
     // No finite or +inf value yet; a NaN would otherwise be skipped by the max.
 #pragma unroll
-    for (int k = 0; k < TL::K; ++k) s.flag |= is_nan(p[k]) ? 1 : 0;
+    for (int u = 0; u < UNROLL; ++u) {
+      float p[TL::VEC];
+      terms(u, p);
+#pragma unroll
+      for (int j = 0; j < TL::VEC; ++j) s.flag |= is_nan(p[j]) ? 1 : 0;
+    }
   } else {
     const float ml = mn * kLog2e;
     // |m| above ~2.3e38 overflows m*log2e: route the row to the exact (subtracting) path.
     if (!is_finite(ml) && is_finite(mn)) s.flag = 1;
     float a = s.acc * fast_exp(s.m - mn);
 #pragma unroll
-    for (int k = 0; k < TL::K; ++k) {
-      if constexpr (CENTERED) a += __builtin_amdgcn_exp2f((p[k] - mn) * kLog2e);
-      else a += __builtin_amdgcn_exp2f(__builtin_fmaf(p[k], kLog2e, -ml));
+    for (int u = 0; u < UNROLL; ++u) {
+      float p[TL::VEC];
+      terms(u, p);
+#pragma unroll
+      for (int j = 0; j < TL::VEC; ++j) {
+        if constexpr (CENTERED) a += __builtin_amdgcn_exp2f((p[j] - mn) * kLog2e);
+        else a += __builtin_amdgcn_exp2f(__builtin_fmaf(p[j], kLog2e, -ml));
+      }
     }
     s.acc = a;
     s.m = mn;
@@ -392,33 +456,40 @@ __device__ __forceinline__ LogLane log_row_combine(LogLane s, LogLane* lds) {
 // ---------------------------------------------------------------- kernel bodies
 // Serial plan: one output per row (template.py:41-54).  WG threads per workgroup, WG/TPR rows
 // per workgroup (one row when TPR >= WG).
-// The row's fp32 result in every lane of the row (fast exponential path with the exact
-// fallback for NaN/+inf rows, or the exact state for other folds).  Every thread of the
-// workgroup must call it (it synchronises when a row spans several wavefronts).
+// The row's fp32 result in every lane of the row from the lanes' fast exponential states,
+// with the exact fallback for rows that met NaN or +inf: exact(bad) returns the row's exact
+// state (a lane passes bad = false to take part in the row's synchronisation only).  Every
+// thread of the workgroup must call it (it synchronises when a row spans several wavefronts).
+template <class F, int TPR, class Exact>
+__device__ __forceinline__ float log_row_result(LogLane s, float n, LogLane* lds_lane,
+                                                Exact exact) {
+  float result;
+  s = log_row_combine<F, TPR>(s, lds_lane);
+  const bool bad = s.flag != 0 || is_nan(s.acc);
+  // Rows with NaN/+inf take the exact reference path; `bad` is uniform across the row.
+  bool any_bad = bad;
+  if constexpr (TPR > 64) {
+    any_bad = __syncthreads_or(bad ? 1 : 0) != 0;
+  } else {
+    any_bad = __builtin_amdgcn_ballot_w64(bad) != 0;
+  }
+  if (any_bad) {
+    const State e = exact(bad);
+    if (bad) result = finalize_state<F>(e, n);
+  }
+  if (!bad) result = (s.m == -kInf) ? -kInf : F::finalize(s.m, s.acc, n);
+  return result;
+}
+
+// The same with the exact path re-reading the row from memory.
 template <class F, class St, int TPR, int UNROLL, bool VECTOR>
 __device__ __forceinline__ float log_row_finish(LogLane s, const typename St::T* rp,
                                                 i64 stride_col, i64 c1, int t, float n,
                                                 State* lds_state, LogLane* lds_lane) {
-  float result;
-  {
-    s = log_row_combine<F, TPR>(s, lds_lane);
-    const bool bad = s.flag != 0 || is_nan(s.acc);
-    // Rows with NaN/+inf take the exact reference path; `bad` is uniform across the row.
-    bool any_bad = bad;
-    if constexpr (TPR > 64) {
-      any_bad = __syncthreads_or(bad ? 1 : 0) != 0;
-    } else {
-      any_bad = __builtin_amdgcn_ballot_w64(bad) != 0;
-    }
-    if (any_bad) {
-      const State e = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, 0,
-                                                                   bad ? c1 : 0, t, n,
-                                                                   lds_state);
-      if (bad) result = finalize_state<F>(e, n);
-    }
-    if (!bad) result = (s.m == -kInf) ? -kInf : F::finalize(s.m, s.acc, n);
-  }
-  return result;
+  return log_row_result<F, TPR>(s, n, lds_lane, [&](bool bad) {
+    return exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, 0, bad ? c1 : 0, t, n,
+                                                       lds_state);
+  });
 }
 
 template <class F, class St, int TPR, int UNROLL, bool VECTOR, bool CENTERED = false>
@@ -459,10 +530,13 @@ __device__ __forceinline__ void fold_serial(const typename St::T* __restrict__ x
 // Readout of an exponential fold (log-softmax for logsumexp): out[row, c] = phi(x[row, c]) -
 // r, r the row's fp32 result, computed in fp32 and rounded once to the storage type; with
 // NAN_POSINF a row whose r is +inf (a +inf element) reads out NaN everywhere, as the lowered
-// `where(lse == inf, nan, x - lse)` does.  `out` is contiguous [rows, ncols].  A row that
-// fits in one tile stays in registers between the fold and the readout (one HBM read);
-// wider rows are read twice.
-template <class F, class St, int TPR, int UNROLL, bool VECTOR, int WG, bool NAN_POSINF>
+// `where(lse == inf, nan, x - lse)` does.  `out` is contiguous [rows, ncols].  RESIDENT
+// kernels take rows that fit in one tile (ncols <= TPR * UNROLL * VEC, checked by the host),
+// which stay in registers between the fold and the readout (one HBM read); the others take
+// any width and read the row twice.  The two are separate kernels so that each is allocated
+// the registers of its own path.
+template <class F, class St, int TPR, int UNROLL, bool VECTOR, int WG, bool NAN_POSINF,
+          bool RESIDENT>
 __device__ __forceinline__ void fold_readout(const typename St::T* __restrict__ x,
                                              typename St::T* __restrict__ out, i64 rows,
                                              i64 ncols, i64 stride_row, i64 stride_col) {
@@ -473,13 +547,14 @@ __device__ __forceinline__ void fold_readout(const typename St::T* __restrict__ 
   __shared__ State lds_state[WG / 64];
   __shared__ LogLane lds_lane[WG / 64];
   const int t = threadIdx.x % TPR;
-  const i64 row = (i64)blockIdx.x * RPW + threadIdx.x / TPR;
+  // one row per workgroup: the row, and so its base addresses, are wave-uniform
+  const i64 row = RPW == 1 ? (i64)blockIdx.x : (i64)blockIdx.x * RPW + threadIdx.x / TPR;
   const bool live = row < rows;
   const typename St::T* rp = x + (live ? row : 0) * stride_row;
   typename St::T* op = out + (live ? row : 0) * ncols;
   const i64 c1 = live ? ncols : 0;
   const float n = (float)ncols;
-  if (ncols <= TL::TILE) {
+  if constexpr (RESIDENT) {
     RawTile<St, UNROLL, VECTOR> keep;
     load_raw<St, TPR, UNROLL, VECTOR>(keep, rp, stride_col, 0, c1, t);
     LogLane s;
@@ -487,9 +562,28 @@ __device__ __forceinline__ void fold_readout(const typename St::T* __restrict__ 
     s.acc = 0.0f;
     s.flag = 0;
     log_fold_tile<F, St, TPR, UNROLL, VECTOR, true>(s, keep, n);
-    const float r = log_row_finish<F, St, TPR, UNROLL, VECTOR>(s, rp, stride_col, c1, t, n,
-                                                               lds_state, lds_lane);
-    const bool nan_row = NAN_POSINF && r == kInf;
+    // The exact fallback takes the row from the registers too: its state equals
+    // exact_row_state's over the one tile (same slots, same order), without a second set of
+    // fp32 values live beside `keep`.
+    const float r = log_row_result<F, TPR>(s, n, lds_lane, [&](bool bad) {
+      State e = empty_state<F>();
+      if (bad) {
+        auto slot = [&](int u, float* w) {
+          if constexpr (VECTOR) {
+            St::reunpack(keep.w[u], w);
+          } else {
+            w[0] = keep.s[u];
+          }
+          return keep.ok[u];
+        };
+        e = merge_state<F>(e, log_chunk<F, UNROLL, TL::VEC>(slot, n));
+      }
+      return row_state<F, TPR>(e, lds_state);
+    });
+    // A NaN row reads out phi(x) - NaN: NaN everywhere (such a row holds no NaN of its own,
+    // which would have made r NaN), without a select per element.
+    const float rr = (NAN_POSINF && r == kInf) ? __builtin_nanf("") : r;
+    reopen(keep);
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       if (!keep.ok[u]) continue;
@@ -498,33 +592,30 @@ __device__ __forceinline__ void fold_readout(const typename St::T* __restrict__ 
         float v[TL::VEC];
         St::unpack(keep.w[u], v);
 #pragma unroll
-        for (int j = 0; j < TL::VEC; ++j)
-          v[j] = nan_row ? __builtin_nanf("") : (F::phi(v[j], n) - r);
-        store16(op + e, St::pack(v));
+        for (int j = 0; j < TL::VEC; ++j) v[j] = F::phi(v[j], n) - rr;
+        store16(op + (u32)((u * TPR + t) * TL::VEC), St::pack(v));
       } else {
-        St::store(op + e, nan_row ? __builtin_nanf("") : (F::phi(keep.s[u], n) - r));
+        St::store(op + e, F::phi(keep.s[u], n) - rr);
       }
     }
-    return;
-  }
-  const float r = row_result<F, St, TPR, UNROLL, VECTOR, true>(rp, stride_col, c1, t, n,
-                                                              lds_state, lds_lane);
-  const bool nan_row = NAN_POSINF && r == kInf;
-  for (i64 tile = 0; tile < c1; tile += TL::TILE) {
+  } else {
+    const float r = row_result<F, St, TPR, UNROLL, VECTOR, true>(rp, stride_col, c1, t, n,
+                                                                lds_state, lds_lane);
+    const float rr = (NAN_POSINF && r == kInf) ? __builtin_nanf("") : r;
+    for (i64 tile = 0; tile < c1; tile += TL::TILE) {
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const i64 e = tile + (i64)(u * TPR + t) * TL::VEC;
-      if (e >= c1) continue;
-      if constexpr (VECTOR) {
-        float v[TL::VEC];
-        St::unpack(load16(rp + e), v);
+      for (int u = 0; u < UNROLL; ++u) {
+        const i64 e = tile + (i64)(u * TPR + t) * TL::VEC;
+        if (e >= c1) continue;
+        if constexpr (VECTOR) {
+          float v[TL::VEC];
+          St::unpack(load16(rp + e), v);
 #pragma unroll
-        for (int j = 0; j < TL::VEC; ++j)
-          v[j] = nan_row ? __builtin_nanf("") : (F::phi(v[j], n) - r);
-        store16(op + e, St::pack(v));
-      } else {
-        const float v = St::load(rp + e * stride_col);
-        St::store(op + e, nan_row ? __builtin_nanf("") : (F::phi(v, n) - r));
+          for (int j = 0; j < TL::VEC; ++j) v[j] = F::phi(v[j], n) - rr;
+          store16(op + e, St::pack(v));
+        } else {
+          St::store(op + e, F::phi(St::load(rp + e * stride_col), n) - rr);
+        }
       }
     }
   }

@@ -180,6 +180,7 @@ def emit_fold_policy(sk: Skeleton, values: dict | None = None, *, struct_name: s
   static constexpr bool kConsumerMax = {str(sk.consumer_reducer == "max").lower()};
   static constexpr bool kFloor = {str(bool(floor)).lower()};
   static constexpr bool kHasBias = {str(bool(has_bias)).lower()};
+  static constexpr bool kPhiIdentity = {str(phi.replace("(", "").replace(")", "").strip() == "v").lower()};
   __device__ static __forceinline__ float phi(float v, float n) {{ return {phi}; }}
   __device__ static __forceinline__ float term(float v, float den, float n) {{ return {term}; }}
   __device__ static __forceinline__ float rho(float q, float q2) {{ return {rho}; }}
@@ -282,8 +283,18 @@ def emit_kernel_source(sk: Skeleton, values: dict | None = None, *, plan: str = 
     return "\n".join(parts)
 
 
-def readout_kernel_name(sk: Skeleton, var: FoldVariant, nan_posinf_rows: bool) -> str:
-    return f"{sk.name}_readout{'_nanrows' if nan_posinf_rows else ''}_{var.tag()}"
+def readout_kernel_name(sk: Skeleton, var: FoldVariant, nan_posinf_rows: bool,
+                        resident: bool = False) -> str:
+    """`resident`: the kernel for rows that fit one tile (readout_tile), which keeps the row in
+    registers; the other kernel takes any width and reads the row twice."""
+    return (f"{sk.name}_readout{'_nanrows' if nan_posinf_rows else ''}_{var.tag()}"
+            f"{'_resident' if resident else ''}")
+
+
+def readout_tile(var: FoldVariant) -> int:
+    """Columns of one tile of a readout launch shape (lanes x slots x elements per slot)."""
+    per_slot = (4 if dtype_tag(var.dtype)[0] == "f32" else 8) if var.vector else 1
+    return var.tpr * var.unroll * per_slot
 
 
 def emit_readout_source(sk: Skeleton, values: dict | None = None, *, variants: tuple,
@@ -301,14 +312,16 @@ def emit_readout_source(sk: Skeleton, values: dict | None = None, *, variants: t
     for var in variants:
         _, st = dtype_tag(var.dtype)
         vec = "true" if var.vector else "false"
-        name = readout_kernel_name(sk, var, nan_posinf_rows)
-        if name in seen:
-            continue
-        seen.add(name)
-        parts.append(
-            f'extern "C" __global__ void __launch_bounds__({var.wg}) {name}({_FOLD_ARGS_SERIAL}) {{\n'
-            f"  nep::fold_readout<Fold, {st}, {var.tpr}, {var.unroll}, {vec}, {var.wg}, {flag}>("
-            f"(const {st}::T*)x, ({st}::T*)out, rows, ncols, stride_row, stride_col);\n}}\n")
+        for resident in (True, False):
+            name = readout_kernel_name(sk, var, nan_posinf_rows, resident)
+            if name in seen:
+                continue
+            seen.add(name)
+            parts.append(
+                f'extern "C" __global__ void __launch_bounds__({var.wg}) {name}({_FOLD_ARGS_SERIAL}) {{\n'
+                f"  nep::fold_readout<Fold, {st}, {var.tpr}, {var.unroll}, {vec}, {var.wg}, {flag}, "
+                f"{'true' if resident else 'false'}>("
+                f"(const {st}::T*)x, ({st}::T*)out, rows, ncols, stride_row, stride_col);\n}}\n")
     return "\n".join(parts)
 
 

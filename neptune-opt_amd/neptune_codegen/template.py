@@ -19,7 +19,7 @@ from neptune_codegen.autotune import (MAX_TPR, MAX_UNROLL, UNROLL, WIDE_16BIT_RO
 from neptune_codegen.emitters import (BASE_OPTIONS, NO_CONTRACT, FoldVariant, RowVariant,
                                       check_supported, emit_kernel_source, emit_readout_source,
                                       emit_rms_state_source, fold_kernel_name,
-                                      readout_kernel_name, rms_kernel_names)
+                                      readout_kernel_name, readout_tile, rms_kernel_names)
 from neptune_codegen.skeleton import SKELETONS, all_registered, param_defaults
 
 MAX_SPLIT_PARTS = 4096
@@ -132,8 +132,9 @@ class ReadoutProgram:
             self._programs[var] = prog
         return prog
 
-    def kernel(self, var: FoldVariant, device: int) -> hip.Kernel:
-        name = readout_kernel_name(self.sk, var, self.nan_posinf_rows)
+    def kernel(self, var: FoldVariant, device: int, resident: bool = False) -> hip.Kernel:
+        """`resident` selects the kernel for rows of at most readout_tile(var) columns."""
+        name = readout_kernel_name(self.sk, var, self.nan_posinf_rows, resident)
         return self.program(var).kernel(name, (hip.PTR, hip.PTR) + (hip.I64,) * 4, var.wg, device)
 
 
@@ -160,7 +161,7 @@ def launch_readout(program: ReadoutProgram, x2, out, rows, ncols, block, num_war
     device = x2.device.index if x2.device.index is not None else torch.cuda.current_device()
     var = _fold_variant(x2, ncols, block, num_warps, resident=True)
     rpw = max(1, var.wg // var.tpr)
-    program.kernel(var, device).launch(
+    program.kernel(var, device, resident=ncols <= readout_tile(var)).launch(
         (_grid_1d(rows, rpw),),
         (x2.data_ptr(), out.data_ptr(), rows, ncols, x2.stride(0), x2.stride(1)),
         hip.current_stream(x2.device))
