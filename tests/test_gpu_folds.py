@@ -303,6 +303,65 @@ def test_log_softmax_readout_nonfinite_rows():
     torch.testing.assert_close(plain[ok], want_plain[ok], rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("width", [300, 40000])
+def test_log_softmax_readout_huge_finite_rows(dtype, width):
+    """Rows whose max exceeds ~2.3e38 (m * log2(e) overflows fp32) take the exact fallback,
+    in the resident kernel (width 300: from the registers it holds) and in the two-read kernel
+    (width 40000): the result is the fp64 log-softmax rounded to the dtype."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(4, width, generator=g)
+    x[0, 5] = 3.0e38
+    x[1, width - 1] = -3.0e38
+    x[1, 2] = 2.5e38
+    x[2, :] = 3.0e38
+    x = x.to(dtype)
+    _say(f"log_softmax readout huge rows {dtype} width {width}")
+    got = CG.run_log_softmax(x.to(dev)).cpu()
+    z = x.double()
+    want = (z - torch.logsumexp(z, -1, keepdim=True)).to(dtype)   # -3e38 - 2.5e38 is -inf
+    assert not torch.isnan(got).any()
+    torch.testing.assert_close(got.float(), want.float(), **dict(zip(("rtol", "atol"), TOL[dtype])))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_readout_resident_and_two_read_kernels_agree_bit_for_bit(dtype):
+    """For one launch shape the resident kernel (row held in registers) and the two-read kernel
+    fold the same slots in the same order, so their outputs are identical; rows include -inf,
+    +inf (read out NaN) and NaN."""
+    from neptune_codegen import hip
+    from neptune_codegen import template as T
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(24)
+    rows, width = 37, 3000
+    x = (4 * torch.randn(rows, width, generator=g))
+    x[3, 10] = float("inf")
+    x[4, 11] = float("nan")
+    x[5, :100] = float("-inf")
+    x = x.to(dtype).to(dev)
+    prog = CG.compile_readout("logsumexp")
+    block, warps = CG.best_config(rows, width, x.dtype, x.device)
+    var = T._fold_variant(x, width, block, warps, resident=True)
+    assert width <= T.readout_tile(var)
+    outs = []
+    for resident in (True, False):
+        out = torch.empty_like(x)
+        _say(f"readout kernel resident={resident} {dtype} {var.tag()}")
+        prog.kernel(var, 0, resident=resident).launch(
+            (T._grid_1d(rows, max(1, var.wg // var.tpr)),),
+            (x.data_ptr(), out.data_ptr(), rows, width, x.stride(0), x.stride(1)),
+            hip.current_stream(x.device))
+        outs.append(out)
+    torch.cuda.synchronize()
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(outs[0].view(bits), outs[1].view(bits))
+    # run_log_softmax picks the same launch shape and, for this width, the resident kernel
+    assert torch.equal(outs[0].view(bits), CG.run_log_softmax(x).view(bits))
+    assert torch.isnan(outs[0][3]).all() and torch.isnan(outs[0][4]).all()
+
+
 def test_log_softmax_graph_through_apply():
     """neptune_opt.apply with the experimental log_softmax lowering runs one readout op on the
     device and verifies against torch (16-bit outputs within 2 ULP)."""
