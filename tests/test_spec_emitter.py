@@ -167,3 +167,37 @@ def test_param_bindings_is_exported_and_bakes_fp32_literals():
     assert {str(k): v for k, v in CG.param_bindings(CG.SKELETONS["variance"]).items()} == {"N": "n"}
     with pytest.raises(KeyError, match="beta"):
         CG.param_bindings(CG.SKELETONS["softcap_lse"], {"tiny": 0.0})
+
+
+def test_readout_source_holds_a_resident_and_a_two_read_kernel_per_shape():
+    """Each readout launch shape is emitted twice: the resident kernel (rows of at most
+    readout_tile columns, held in registers) and the two-read kernel (any width)."""
+    var = E.FoldVariant("bfloat16", True, 512, 8, 8)
+    assert E.readout_tile(var) == 512 * 8 * 8
+    assert E.readout_tile(E.FoldVariant("float32", True, 256, 4, 4)) == 256 * 4 * 4
+    assert E.readout_tile(E.FoldVariant("float16", False, 64, 8, 1)) == 64 * 8
+    sk = CG.SKELETONS["logsumexp"]
+    src = E.emit_readout_source(sk, CG.param_defaults("logsumexp"), variants=(var,))
+    resident = E.readout_kernel_name(sk, var, True, True)
+    two_read = E.readout_kernel_name(sk, var, True, False)
+    assert resident == two_read + "_resident"
+    assert f"{resident}(" in src and f"{two_read}(" in src
+    assert src.count("nep::fold_readout<") == 2
+
+
+def test_row_variant_rule_for_16_bit_rows():
+    """RMS / L2 launch shapes: 4 slots per lane for 16-bit rows of 2048-8192 elements, 2 at
+    1024, 8 otherwise (fp32 rows keep 8)."""
+    import torch
+
+    from neptune_codegen import template as T
+
+    want = {1000: (16, 8), 1024: (64, 2), 2048: (64, 4), 4096: (128, 4), 8192: (256, 4),
+            16384: (256, 8), 32768: (512, 8)}
+    for width, (tpr, nv) in want.items():
+        x = torch.empty(4, width, dtype=torch.bfloat16, device="meta")
+        var = T._row_variant(x, None, width)
+        assert (var.tpr, var.nv, var.vector) == (tpr, nv, True), width
+        assert var.tpr * var.nv * 8 >= width
+    x = torch.empty(4, 4096, dtype=torch.float32, device="meta")
+    assert T._row_variant(x, None, 4096).nv == 8
