@@ -326,17 +326,6 @@ __device__ __forceinline__ void load_raw(RawTile<St, UNROLL, VECTOR>& r,
   }
 }
 
-// One lane's exponential fold over its slots of [c0, c1).  The next tile's loads are issued
-// before the current tile is folded, so each lane keeps up to 2*UNROLL loads in flight.
-// Per element: one max, one fma for the base-2 exponent, one exp2, one add.  The exponent
-// p*log2e - m*log2e carries an absolute error of about |m| * 2^-23, which is relative to the
-// readout m + log(acc): the row result keeps ~1e-7 relative accuracy.
-//
-// CENTERED evaluates exp2((p - m) * log2e) instead: p - m is exact, so an element equal to the
-// row maximum contributes exactly 1 (one more VALU op per element).  The readout uses it, so
-// that a log-probability of 0 comes out as 0 rather than as the rounding residue of m*log2e.
-// Fold one raw tile into a lane's exponential state.
-//
 // The held words of a raw tile, made opaque to the compiler: unpacks after this point cannot
 // reuse values unpacked before it, so a pass over a held row re-derives its fp32 values from
 // the 16-bit words instead of keeping them live (no instruction is emitted).
@@ -348,11 +337,18 @@ __device__ __forceinline__ void reopen(RawTile<St, UNROLL, VECTOR>& r) {
   }
 }
 
-// The centred (readout) fold holds a whole row per lane group and keeps the raw words for the
-// readout, so it recomputes phi from them in each pass rather than holding the K fp32 terms
-// across the max (K = 64 for a 16-bit row of 8 slots: 64 VGPRs, which would cut the readout
-// to one 8-wave workgroup per CU).  The terms and their order are the same, so results are
-// unchanged.
+// Fold one raw tile into a lane's exponential state.  Per element: one max, one fma for the
+// base-2 exponent, one exp2, one add.  The exponent p*log2e - m*log2e carries an absolute
+// error of about |m| * 2^-23, which is relative to the readout m + log(acc): the row result
+// keeps ~1e-7 relative accuracy.
+//
+// CENTERED evaluates exp2((p - m) * log2e) instead: p - m is exact, so an element equal to the
+// row maximum contributes exactly 1 (one more VALU op per element).  The readout uses it, so
+// that a log-probability of 0 comes out as 0 rather than as the rounding residue of m*log2e.
+// The readout also holds its whole row in the raw words, so the centred fold recomputes phi
+// from them in each pass rather than holding the K fp32 terms across the max (K = 64 for a
+// 16-bit row of 8 slots: 64 VGPRs, which would cut the readout to one 8-wave workgroup per
+// CU); the terms and their order are the same.
 template <class F, class St, int TPR, int UNROLL, bool VECTOR, bool CENTERED>
 __device__ __forceinline__ void log_fold_tile(LogLane& s, RawTile<St, UNROLL, VECTOR>& cur,
                                               float n) {
@@ -406,6 +402,8 @@ __device__ __forceinline__ void log_fold_tile(LogLane& s, RawTile<St, UNROLL, VE
   }
 }
 
+// One lane's exponential fold over its slots of [c0, c1).  The next tile's loads are issued
+// before the current tile is folded, so each lane keeps up to 2*UNROLL loads in flight.
 template <class F, class St, int TPR, int UNROLL, bool VECTOR, bool CENTERED = false>
 __device__ __forceinline__ LogLane log_row_lane(const typename St::T* row, i64 stride_col,
                                                 i64 c0, i64 c1, int t, float n) {
