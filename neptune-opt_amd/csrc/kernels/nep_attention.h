@@ -1,4 +1,5 @@
-// nep_attention.h -- causal online-softmax attention fold on gfx950 MFMA (bf16 in, fp32 acc).
+// nep_attention.h -- causal online-softmax attention fold on gfx950 MFMA (bf16 or fp16 in,
+// fp32 accumulation).
 //
 // O = softmax(scale * Q K^T + causal mask) V per (batch, head), evaluated as a fold over key
 // tiles with the logsumexp repair: running max m, running sum l and accumulator O are moved to
@@ -6,20 +7,23 @@
 // materialised.  Scores live in the base-2 domain t = scale*log2(e) * q.k.
 //
 // Two kernels per call:
-//  * attention_vt_pack: V [key][dim] bf16 -> per key tile a V^T image in fp16 (the exact MFMA
+//  * attention_vt_pack: V [key][dim] -> per key tile a V^T image in fp16 (the exact MFMA
 //    operand order, XOR-swizzled for conflict-free LDS reads) plus one power-of-two exponent
-//    per tile.  Tiles whose largest |v| reaches 2^15 are stored as v * 2^-e (exact: bf16
-//    values keep their 8 significant bits in fp16 down to |v| >= 2^(e-17)); the fold feeds
+//    per tile.  Tiles whose largest finite |v| reaches 2^15 are stored as v * 2^-e (exact: a
+//    16-bit input keeps its significant bits in fp16 down to |v| >= 2^(e-14)); the fold feeds
 //    such a tile P * 2^e instead of P and weights its row sum by 2^-e, both exact, so no
 //    accumulator is rescaled.  A tile value below 2^(e-14) keeps an absolute precision of
-//    2^(e-25) only, so the caller bounds e (e_max); a tile above it, or holding inf/NaN,
-//    clears *status, which the caller turns into an error.  The image is written once per
-//    call and read by every query block of the head.
+//    2^(e-25) only, so the fold takes tiles with e <= e_max on this path.  The stored exponent
+//    is the tile's own (kVtNonFinite for a tile holding inf or NaN).  The image is written
+//    once per call and read by every query block of the head.
 //  * attention_fwd: one workgroup = 8 wave64s = BLOCK_M = 256 queries (32 per wave), one
 //    workgroup per CU (two waves per SIMD): each staged K / V^T tile serves 256 queries.
-//    K (bf16, the caller's strided rows, bounds-checked buffer loads) and the V^T image go
+//    K (the caller's strided rows, bounds-checked buffer loads) and the V^T image go
 //    straight from HBM into double-buffered LDS (buffer_load ... lds, no registers): tile t+1
-//    is in flight while tile t is computed, with one barrier per tile.
+//    is in flight while tile t is computed, with one barrier per tile.  A workgroup that read
+//    a tile exponent above e_max (|v| >= 2^(e_max+15), inf or NaN in V) recomputes its
+//    queries with attention_exact_rows instead: fp32 scores, fp32 P and the caller's V, so
+//    every input has a defined result without a device-side trap or a host round trip.
 //
 // MFMA mapping (v_mfma_f32_32x32x16_{bf16,f16}):
 //  * S^T = K Q^T: A = K rows (key = lane%32, 8 consecutive head dims per lane from LDS),
@@ -32,7 +36,8 @@
 //  * P V in fp16 (unit roundoff 2^-11, 8x finer than bf16 for P).
 //  * Lazy rescaling: the reference max only moves when the running max exceeds it by more than
 //    8 (base 2), so P <= 256 (exact range of fp16) and O is rescaled on few tiles.
-//  * The row sum l accumulates the fp16-rounded P with v_dot2 (the values the MFMA multiplies).
+//  * The row sum l accumulates the fp32 P (before its fp16 rounding), so the logsumexp side
+//    output carries fp32 accuracy; O is normalised by the same l.
 //  * Tiles above the causal diagonal are skipped per wave; workgroups run heaviest query block
 //    first and a head's blocks share one XCD (workgroup id % 8 == head % 8), so its K and V^T
 //    stay in that XCD's L2.
@@ -52,7 +57,9 @@ constexpr int kAttnBN = 64;            // keys per tile
 constexpr int kAttnThreads = 256;      // V^T pack workgroup: 4 wave64s
 constexpr float kRescaleSlack = 8.0f;  // base-2 headroom before the reference max moves
 constexpr u32 kRawBufferWord3 = 0x00020000u;   // gfx9 raw buffer descriptor, dword 3
-constexpr u32 kVtScaleFrom = 142u;     // bf16 biased exponent of 2^15: tiles at or above scale
+constexpr u32 kVtScaleFrom = 142u;     // fp32 biased exponent of 2^15: tiles at or above scale
+constexpr int kVtNonFinite = 255;      // tile exponent recorded for a tile holding inf or NaN
+constexpr int kVtExpClamp = 24;        // largest exponent the fold's scaling arithmetic takes
 
 __device__ __forceinline__ u32 pack_bf16x2(float a, float b) {
   f32x2 f = {a, b};
@@ -66,6 +73,31 @@ __device__ __forceinline__ u32 pack_f16x2(float a, float b) {
 }
 // 2^k for |k| <= 126 (exact, built from the exponent field)
 __device__ __forceinline__ float exp2_int(int k) { return as_f32((u32)(127 + k) << 23); }
+
+// The 16-bit input types: widening of the low / high element of a packed pair, RNE packing of
+// two fp32 values, the 8-element MFMA operand and the QK^T MFMA of that type.
+template <typename T>
+struct AttnIn;
+template <>
+struct AttnIn<__bf16> {
+  typedef bf16x8 vec8;
+  __device__ static __forceinline__ float lo(u32 w) { return as_f32(w << 16); }
+  __device__ static __forceinline__ float hi(u32 w) { return as_f32(w & 0xffff0000u); }
+  __device__ static __forceinline__ u32 pack2(float a, float b) { return pack_bf16x2(a, b); }
+  __device__ static __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct AttnIn<_Float16> {
+  typedef f16x8 vec8;
+  __device__ static __forceinline__ float lo(u32 w) { return (float)as_half2(w)[0]; }
+  __device__ static __forceinline__ float hi(u32 w) { return (float)as_half2(w)[1]; }
+  __device__ static __forceinline__ u32 pack2(float a, float b) { return pack_f16x2(a, b); }
+  __device__ static __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
 
 // Position (0..63, before the row swizzle) of tile key `key` in a V^T image row: chunk
 // j = 2*(key/16) + (key/4)%2 holds keys 16*(j/2) + 4*(j%2) + {0,1,2,3} and the same + 8, which
@@ -86,27 +118,31 @@ __device__ __forceinline__ int swizzle(int row) {
   else return (row >> 1) & 7;
 }
 
-// V bf16 [keys, D] of one head -> fp16 V^T tile images [ntiles][D][64] (16-byte chunk j of row
-// d stored at chunk j ^ swizzle<8>(d)) and one exponent per tile.  Keys past sk are zero.
-template <int D>
-__device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
-                                                  u16* __restrict__ vt, int* __restrict__ exps,
-                                                  int* __restrict__ status, int e_max,
-                                                  int heads, int sk, i64 vsb, i64 vsh, i64 vss) {
+// V [keys, D] of one head -> fp16 V^T tile images [ntiles][D][64] (16-byte chunk j of row d
+// stored at chunk j ^ swizzle<8>(d)) and one exponent per tile: 0 below 2^15, e for a largest
+// finite |v| in [2^(14+e), 2^(15+e)), kVtNonFinite for a tile holding inf or NaN.  The image
+// of a tile is scaled by 2^-min(e, kVtExpClamp).  Keys past sk are zero.
+template <typename T, int D>
+__device__ __forceinline__ void attention_vt_pack(const T* __restrict__ v, u16* __restrict__ vt,
+                                                  int* __restrict__ exps, int heads, int sk,
+                                                  i64 vsb, i64 vsh, i64 vss) {
+  typedef AttnIn<T> In;
   constexpr int CH = D / 8;                         // 16-byte chunks per key row
   constexpr int UNITS = (kAttnBN / 2) * CH;         // (key pair, dim chunk) units
   constexpr int UPT = UNITS / kAttnThreads;
   static_assert(UNITS % kAttnThreads == 0, "head dim must be 64 or 128");
   __shared__ __attribute__((aligned(16))) u16 img[D * kAttnBN];
   __shared__ u32 wave_max[kAttnThreads / 64];
+  __shared__ int wave_bad[kAttnThreads / 64];
   const int ntiles = (sk + kAttnBN - 1) / kAttnBN;
   const int bh = blockIdx.x / ntiles, t = blockIdx.x % ntiles;
   const int b = bh / heads, h = bh % heads;
-  const __bf16* vp = v + b * vsb + h * vsh;
+  const T* vp = v + b * vsb + h * vsh;
   const int k0 = t * kAttnBN, tid = threadIdx.x;
 
   u32x4 raw[UPT][2];
-  u32 mx = 0;
+  u32 mx = 0;      // largest finite magnitude (fp32 bits: integer order = magnitude order)
+  int bad = 0;     // a non-finite value in the tile
 #pragma unroll
   for (int u = 0; u < UPT; ++u) {
     const int unit = tid + u * kAttnThreads, kp = unit / CH, ch = unit % CH;
@@ -116,26 +152,30 @@ __device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
       raw[u][r] = key < sk ? load16_cached(vp + (i64)key * vss + ch * 8) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const u32 x = raw[u][r][w] & 0x7fff7fffu;
-        mx = max(mx, max(x & 0xffffu, x >> 16));
+        const u32 a = as_u32(In::lo(raw[u][r][w])) & 0x7fffffffu;
+        const u32 c = as_u32(In::hi(raw[u][r][w])) & 0x7fffffffu;
+        bad |= (a >= 0x7f800000u) | (c >= 0x7f800000u);
+        mx = max(mx, max(a < 0x7f800000u ? a : 0u, c < 0x7f800000u ? c : 0u));
       }
     }
   }
-  // largest bf16 magnitude of the tile (integer order = magnitude order, NaN above inf)
   mx = max(mx, partner_u32<1>(mx));
   mx = max(mx, partner_u32<2>(mx));
   mx = max(mx, partner_u32<4>(mx));
   mx = max(mx, partner_u32<8>(mx));
   mx = max(mx, partner_u32<16>(mx));
   mx = max(mx, partner_u32<32>(mx));
-  if ((tid & 63) == 0) wave_max[tid >> 6] = mx;
+  bad = group_or<64>(bad);
+  if ((tid & 63) == 0) {
+    wave_max[tid >> 6] = mx;
+    wave_bad[tid >> 6] = bad;
+  }
   __syncthreads();
   mx = max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]));
-  const u32 ebits = mx >> 7;                  // 255: the tile holds inf or NaN
+  bad = wave_bad[0] | wave_bad[1] | wave_bad[2] | wave_bad[3];
+  const u32 ebits = mx >> 23;
   const int e_tile = ebits >= kVtScaleFrom ? (int)(ebits - kVtScaleFrom + 1) : 0;
-  // the fold's scaling arithmetic covers e <= 24; a refused tile is clamped into it
-  const int e = min(e_tile, 24);
-  const float down = exp2_int(-e);
+  const float down = exp2_int(-min(e_tile, kVtExpClamp));
 
 #pragma unroll
   for (int u = 0; u < UPT; ++u) {
@@ -145,9 +185,9 @@ __device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
     for (int d2 = 0; d2 < 8; ++d2) {
       const int dim = ch * 8 + d2;
       const u32 w0 = raw[u][0][d2 >> 1], w1 = raw[u][1][d2 >> 1];
-      const u32 b0 = (d2 & 1) ? (w0 & 0xffff0000u) : (w0 << 16);
-      const u32 b1 = (d2 & 1) ? (w1 & 0xffff0000u) : (w1 << 16);
-      const u32 word = pack_f16x2(as_f32(b0) * down, as_f32(b1) * down);
+      const float f0 = (d2 & 1) ? In::hi(w0) : In::lo(w0);
+      const float f1 = (d2 & 1) ? In::hi(w1) : In::lo(w1);
+      const u32 word = pack_f16x2(f0 * down, f1 * down);
       const int pos = (((slot >> 3) ^ swizzle<8>(dim)) << 3) | (slot & 7);
       *(u32*)(img + dim * kAttnBN + pos) = word;
     }
@@ -157,10 +197,7 @@ __device__ __forceinline__ void attention_vt_pack(const __bf16* __restrict__ v,
 #pragma unroll
   for (int c = tid; c < D * kAttnBN / 8; c += kAttnThreads)
     store16(dst + c * 8, *(const u32x4*)(img + c * 8));
-  if (tid == 0) {
-    exps[bh * ntiles + t] = e;
-    if (e_tile > e_max) *status = 0;
-  }
+  if (tid == 0) exps[bh * ntiles + t] = bad ? kVtNonFinite : e_tile;
 }
 
 // 32-bit LDS address of a pointer into __shared__ memory.
@@ -177,70 +214,81 @@ __device__ __forceinline__ u32 lds_address(const void* p) {
 // (also counted by lgkmcnt, retiring out of order) can be outstanding, and ends with s_nops
 // for the wait states before VALU reads the last MFMA's result.  addr[s] is the LDS address
 // of the k-step s fragment of key block 0; block 1 is 32 rows (8192 bytes) further.
-__device__ __forceinline__ void attention_s_tile_d128(const u32 (&addr)[8], const bf16x8 (&q)[8],
-                                                      f32x16& s0, f32x16& s1) {
-  asm volatile(
-      "s_waitcnt lgkmcnt(0)\n"
-      "ds_read_b128 v[224:227], %[a0]\n"
-      "ds_read_b128 v[228:231], %[a1]\n"
-      "ds_read_b128 v[232:235], %[a2]\n"
-      "ds_read_b128 v[236:239], %[a3]\n"
-      "ds_read_b128 v[240:243], %[a4]\n"
-      "ds_read_b128 v[244:247], %[a5]\n"
-      "ds_read_b128 v[248:251], %[a6]\n"
-      "ds_read_b128 v[252:255], %[a7]\n"
-      "s_waitcnt lgkmcnt(7)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s0], v[224:227], %[q0], 0\n"
-      "s_waitcnt lgkmcnt(6)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s0], v[228:231], %[q1], %[s0]\n"
-      "ds_read_b128 v[224:227], %[a0] offset:8192\n"
-      "s_waitcnt lgkmcnt(6)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s0], v[232:235], %[q2], %[s0]\n"
-      "ds_read_b128 v[228:231], %[a1] offset:8192\n"
-      "s_waitcnt lgkmcnt(6)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s0], v[236:239], %[q3], %[s0]\n"
-      "ds_read_b128 v[232:235], %[a2] offset:8192\n"
-      "s_waitcnt lgkmcnt(6)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s0], v[240:243], %[q4], %[s0]\n"
-      "ds_read_b128 v[236:239], %[a3] offset:8192\n"
-      "s_waitcnt lgkmcnt(6)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s0], v[244:247], %[q5], %[s0]\n"
-      "ds_read_b128 v[240:243], %[a4] offset:8192\n"
-      "s_waitcnt lgkmcnt(6)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s0], v[248:251], %[q6], %[s0]\n"
-      "ds_read_b128 v[244:247], %[a5] offset:8192\n"
-      "s_waitcnt lgkmcnt(6)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s0], v[252:255], %[q7], %[s0]\n"
-      "ds_read_b128 v[248:251], %[a6] offset:8192\n"
-      "s_waitcnt lgkmcnt(6)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s1], v[224:227], %[q0], 0\n"
-      "ds_read_b128 v[252:255], %[a7] offset:8192\n"
-      "s_waitcnt lgkmcnt(6)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s1], v[228:231], %[q1], %[s1]\n"
-      "s_waitcnt lgkmcnt(5)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s1], v[232:235], %[q2], %[s1]\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s1], v[236:239], %[q3], %[s1]\n"
-      "s_waitcnt lgkmcnt(3)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s1], v[240:243], %[q4], %[s1]\n"
-      "s_waitcnt lgkmcnt(2)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s1], v[244:247], %[q5], %[s1]\n"
-      "s_waitcnt lgkmcnt(1)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s1], v[248:251], %[q6], %[s1]\n"
-      "s_waitcnt lgkmcnt(0)\n"
-      "v_mfma_f32_32x32x16_bf16 %[s1], v[252:255], %[q7], %[s1]\n"
-      "s_nop 7\n"
-      "s_nop 7\n"
-      "s_nop 7\n"
-      : [s0] "=&v"(s0), [s1] "=&v"(s1)
-      : [a0] "v"(addr[0]), [a1] "v"(addr[1]), [a2] "v"(addr[2]), [a3] "v"(addr[3]),
-        [a4] "v"(addr[4]), [a5] "v"(addr[5]), [a6] "v"(addr[6]), [a7] "v"(addr[7]),
-        [q0] "v"(q[0]), [q1] "v"(q[1]), [q2] "v"(q[2]), [q3] "v"(q[3]), [q4] "v"(q[4]),
-        [q5] "v"(q[5]), [q6] "v"(q[6]), [q7] "v"(q[7])
-      : "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234",
-        "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245",
+// OP names the MFMA input type (bf16 or f16).
+#define NEP_ATTN_S_TILE_D128(OP) \
+  asm volatile( \
+      "s_waitcnt lgkmcnt(0)\n" \
+      "ds_read_b128 v[224:227], %[a0]\n" \
+      "ds_read_b128 v[228:231], %[a1]\n" \
+      "ds_read_b128 v[232:235], %[a2]\n" \
+      "ds_read_b128 v[236:239], %[a3]\n" \
+      "ds_read_b128 v[240:243], %[a4]\n" \
+      "ds_read_b128 v[244:247], %[a5]\n" \
+      "ds_read_b128 v[248:251], %[a6]\n" \
+      "ds_read_b128 v[252:255], %[a7]\n" \
+      "s_waitcnt lgkmcnt(7)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s0], v[224:227], %[q0], 0\n" \
+      "s_waitcnt lgkmcnt(6)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s0], v[228:231], %[q1], %[s0]\n" \
+      "ds_read_b128 v[224:227], %[a0] offset:8192\n" \
+      "s_waitcnt lgkmcnt(6)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s0], v[232:235], %[q2], %[s0]\n" \
+      "ds_read_b128 v[228:231], %[a1] offset:8192\n" \
+      "s_waitcnt lgkmcnt(6)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s0], v[236:239], %[q3], %[s0]\n" \
+      "ds_read_b128 v[232:235], %[a2] offset:8192\n" \
+      "s_waitcnt lgkmcnt(6)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s0], v[240:243], %[q4], %[s0]\n" \
+      "ds_read_b128 v[236:239], %[a3] offset:8192\n" \
+      "s_waitcnt lgkmcnt(6)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s0], v[244:247], %[q5], %[s0]\n" \
+      "ds_read_b128 v[240:243], %[a4] offset:8192\n" \
+      "s_waitcnt lgkmcnt(6)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s0], v[248:251], %[q6], %[s0]\n" \
+      "ds_read_b128 v[244:247], %[a5] offset:8192\n" \
+      "s_waitcnt lgkmcnt(6)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s0], v[252:255], %[q7], %[s0]\n" \
+      "ds_read_b128 v[248:251], %[a6] offset:8192\n" \
+      "s_waitcnt lgkmcnt(6)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s1], v[224:227], %[q0], 0\n" \
+      "ds_read_b128 v[252:255], %[a7] offset:8192\n" \
+      "s_waitcnt lgkmcnt(6)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s1], v[228:231], %[q1], %[s1]\n" \
+      "s_waitcnt lgkmcnt(5)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s1], v[232:235], %[q2], %[s1]\n" \
+      "s_waitcnt lgkmcnt(4)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s1], v[236:239], %[q3], %[s1]\n" \
+      "s_waitcnt lgkmcnt(3)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s1], v[240:243], %[q4], %[s1]\n" \
+      "s_waitcnt lgkmcnt(2)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s1], v[244:247], %[q5], %[s1]\n" \
+      "s_waitcnt lgkmcnt(1)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s1], v[248:251], %[q6], %[s1]\n" \
+      "s_waitcnt lgkmcnt(0)\n" \
+      "v_mfma_f32_32x32x16_" OP " %[s1], v[252:255], %[q7], %[s1]\n" \
+      "s_nop 7\n" \
+      "s_nop 7\n" \
+      "s_nop 7\n" \
+      : [s0] "=&v"(s0), [s1] "=&v"(s1) \
+      : [a0] "v"(addr[0]), [a1] "v"(addr[1]), [a2] "v"(addr[2]), [a3] "v"(addr[3]), \
+        [a4] "v"(addr[4]), [a5] "v"(addr[5]), [a6] "v"(addr[6]), [a7] "v"(addr[7]), \
+        [q0] "v"(q[0]), [q1] "v"(q[1]), [q2] "v"(q[2]), [q3] "v"(q[3]), [q4] "v"(q[4]), \
+        [q5] "v"(q[5]), [q6] "v"(q[6]), [q7] "v"(q[7]) \
+      : "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234", \
+        "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", \
         "v246", "v247", "v248", "v249", "v250", "v251", "v252", "v253", "v254", "v255", "memory");
+
+template <typename T>
+__device__ __forceinline__ void attention_s_tile_d128(const u32 (&addr)[8],
+                                                      const typename AttnIn<T>::vec8 (&q)[8],
+                                                      f32x16& s0, f32x16& s1) {
+  if constexpr (__is_same(T, __bf16)) {
+    NEP_ATTN_S_TILE_D128("bf16")
+  } else {
+    NEP_ATTN_S_TILE_D128("f16")
+  }
 }
+#undef NEP_ATTN_S_TILE_D128
 
 // LDS-DMA of one tile operand: 16 bytes per lane into 1 KB blocks; piece i of wave w fills
 // block i*W + w (W waves per workgroup).  `dst` is the wave's block (wave-uniform, it becomes M0).
@@ -250,16 +298,105 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* dst, in
       rsrc, (__attribute__((address_space(3))) void*)dst, 16, voffset, soffset, 0, 0);
 }
 
-template <int D, bool CAUSAL>
-__device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
-                                              const __bf16* __restrict__ k,
+// Exact fold of the queries [q0, q0 + kAttnBM) of one head, for a workgroup whose key range
+// holds a V tile the MFMA path does not take (|v| >= 2^(e_max+15), inf or NaN).  fp32
+// throughout: a query's row is held by 4 adjacent lanes (D/4 head dims each); per key the
+// score is the group sum of their partial dot products, and (m, l, O) are moved to every new
+// maximum exactly (not lazily).  Masked keys contribute nothing, so only the rows that see a
+// non-finite V value turn non-finite, as IEEE arithmetic on the visible keys gives.
+template <typename T, int D, bool CAUSAL>
+__device__ void attention_exact_rows(const T* __restrict__ qp, const T* __restrict__ kp,
+                                     const T* __restrict__ vp, T* __restrict__ orow0,
+                                     float* __restrict__ lse_row0, int sq, int sk, int q0,
+                                     i64 qss, i64 kss, i64 vss, float scale_log2) {
+  typedef AttnIn<T> In;
+  constexpr int DQ = D / 4;                    // head dims per lane
+  constexpr int ROWS = kAttnWaves * 64 / 4;    // queries per round
+  const int tid = threadIdx.x, c = tid & 3;
+  for (int r0 = q0; r0 < q0 + kAttnBM; r0 += ROWS) {
+    const int my_q = r0 + (tid >> 2);
+    const bool active = my_q < sq;
+    float qv[DQ], ov[DQ];
+#pragma unroll
+    for (int d8 = 0; d8 < DQ; d8 += 8) {
+      const u32x4 w = active ? load16_cached(qp + (i64)my_q * qss + c * DQ + d8)
+                             : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qv[d8 + 2 * i] = In::lo(w[i]) * scale_log2;
+        qv[d8 + 2 * i + 1] = In::hi(w[i]) * scale_log2;
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) ov[d] = 0.0f;
+    float m = -kInf, l = 0.0f;
+    const int kend = CAUSAL ? min(sk, r0 + ROWS) : sk;
+    const int last = !active ? -1 : (CAUSAL ? min(my_q, sk - 1) : sk - 1);
+#pragma unroll 2
+    for (int j = 0; j < kend; ++j) {
+      const T* kr = kp + (i64)j * kss + c * DQ;
+      const T* vr = vp + (i64)j * vss + c * DQ;
+      u32x4 kw[DQ / 8], vw[DQ / 8];
+#pragma unroll
+      for (int i = 0; i < DQ / 8; ++i) {
+        kw[i] = load16_cached(kr + 8 * i);
+        vw[i] = load16_cached(vr + 8 * i);
+      }
+      float dot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < DQ / 8; ++i)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          dot = __builtin_fmaf(qv[8 * i + 2 * w], In::lo(kw[i][w]), dot);
+          dot = __builtin_fmaf(qv[8 * i + 2 * w + 1], In::hi(kw[i][w]), dot);
+        }
+      const float s = group_sum<4>(dot);   // every lane of the group: the whole score
+      if (j <= last) {
+        if (s > m) {
+          const float alpha = m == -kInf ? 0.0f : __builtin_amdgcn_exp2f(m - s);
+          l *= alpha;
+#pragma unroll
+          for (int d = 0; d < DQ; ++d) ov[d] *= alpha;
+          m = s;
+        }
+        const float p = __builtin_amdgcn_exp2f(s - m);
+        l += p;
+#pragma unroll
+        for (int i = 0; i < DQ / 8; ++i)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            ov[8 * i + 2 * w] = __builtin_fmaf(p, In::lo(vw[i][w]), ov[8 * i + 2 * w]);
+            ov[8 * i + 2 * w + 1] = __builtin_fmaf(p, In::hi(vw[i][w]), ov[8 * i + 2 * w + 1]);
+          }
+      }
+    }
+    if (active) {
+      T* orow = orow0 + (i64)my_q * D + c * DQ;
+#pragma unroll
+      for (int d8 = 0; d8 < DQ; d8 += 8) {
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = In::pack2(ov[d8 + 2 * i] / l, ov[d8 + 2 * i + 1] / l);
+        *(u32x4*)(orow + d8) = w;
+      }
+      if (lse_row0 != nullptr && c == 0)
+        lse_row0[my_q] = (m + __builtin_log2f(l)) * 0.6931471805599453f;
+    }
+  }
+}
+
+template <typename T, int D, bool CAUSAL>
+__device__ __forceinline__ void attention_fwd(const T* __restrict__ q, const T* __restrict__ k,
                                               const u16* __restrict__ vt,
                                               const int* __restrict__ exps,
-                                              __bf16* __restrict__ o, float* __restrict__ lse,
-                                              int heads, int sq, int sk, i64 qsb, i64 qsh,
-                                              i64 qss, i64 ksb, i64 ksh, i64 kss,
+                                              const T* __restrict__ v, T* __restrict__ o,
+                                              float* __restrict__ lse, int heads, int sq, int sk,
+                                              i64 qsb, i64 qsh, i64 qss, i64 ksb, i64 ksh,
+                                              i64 kss, i64 vsb, i64 vsh, i64 vss, int e_max,
                                               float scale_log2) {
   static_assert(D == 64 || D == 128, "head dim must be 64 or 128");
+  typedef AttnIn<T> In;
+  typedef typename In::vec8 vec8;
   constexpr int CH = D / 8;                          // 16-byte chunks per K row
   constexpr int KSTEPS = D / 16;                     // MFMA k-steps of S^T
   constexpr int DBLK = D / 32;                       // 32-row blocks of O^T
@@ -286,18 +423,18 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
   const int ksw = swizzle<CH>(l32), vsw = swizzle<8>(l32);   // rows kb*32 + l32, a*32 + l32
   const int q0 = qb * kAttnBM, qw = q0 + wave * 32;
   const int my_q = qw + l32;
-  const __bf16* qp = q + b * qsb + h * qsh;
-  const __bf16* kp = k + b * ksb + h * ksh;
+  const T* qp = q + b * qsb + h * qsh;
+  const T* kp = k + b * ksb + h * ksh;
   const int ntiles_all = (sk + kAttnBN - 1) / kAttnBN;
   const u16* vth = vt + (i64)bh * ntiles_all * (D * kAttnBN);
   const int* eh = exps + bh * ntiles_all;
 
   // Q^T operand: query my_q, head dims [16s + 8*hi, +8) for k-step s.
-  bf16x8 qreg[KSTEPS];
+  vec8 qreg[KSTEPS];
 #pragma unroll
   for (int s = 0; s < KSTEPS; ++s) {
-    if (my_q < sq) qreg[s] = *(const bf16x8*)(qp + (i64)my_q * qss + 16 * s + 8 * hi);
-    else qreg[s] = bf16x8{};
+    if (my_q < sq) qreg[s] = *(const vec8*)(qp + (i64)my_q * qss + 16 * s + 8 * hi);
+    else qreg[s] = vec8{};
   }
 
   int kv_end = sk;
@@ -335,11 +472,12 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
 #pragma unroll
   for (int a = 0; a < DBLK; ++a) oacc[a] = f32x16{};
   float m_ref = -kInf;   // reference max (base 2) of this lane's query
-  float l_run = 0.0f;
+  float l_even = 0.0f, l_odd = 0.0f;   // row sum of the fp32 P, in two chains
 
-  auto body = [&](int tile, const unsigned char* kt, const unsigned char* vtt, int e) {
+  auto body = [&](int tile, const unsigned char* kt, const unsigned char* vtt, int e_in) {
     const int k0 = tile * kAttnBN;
     if (CAUSAL && k0 > qw + 31) return;   // tile entirely above this wave's diagonal
+    const int e = min(e_in, kVtExpClamp);
     // ---- S^T = K Q^T for the two 32-key blocks of the tile (head dim 128: one instruction
     // block with the K reads ahead of their MFMAs)
     f32x16 sacc[2];
@@ -348,7 +486,7 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
       u32 addr[8];
 #pragma unroll
       for (int s = 0; s < 8; ++s) addr[s] = krow0 + (((2 * s + hi) ^ ksw) << 4);
-      attention_s_tile_d128(addr, qreg, sacc[0], sacc[1]);
+      attention_s_tile_d128<T>(addr, qreg, sacc[0], sacc[1]);
     } else {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -356,8 +494,8 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
         const unsigned char* krow = kt + (kb * 32 + l32) * (CH * 16);
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s) {
-          const bf16x8 a = *(const bf16x8*)(krow + (((2 * s + hi) ^ ksw) << 4));
-          sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[kb], 0, 0, 0);
+          const vec8 a = *(const vec8*)(krow + (((2 * s + hi) ^ ksw) << 4));
+          sacc[kb] = In::mfma(a, qreg[s], sacc[kb]);
         }
       }
     }
@@ -386,14 +524,14 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
     if (__builtin_amdgcn_ballot_w64(move) != 0) {
       const float m_new = move ? tmax + lift : m_ref;
       const float alpha = (m_ref == -kInf) ? 0.0f : __builtin_amdgcn_exp2f(m_ref - m_new);
-      l_run *= alpha;
+      l_even *= alpha;
+      l_odd *= alpha;
 #pragma unroll
       for (int a = 0; a < DBLK; ++a) oacc[a] *= alpha;
       m_ref = m_new;
     }
     const float shift = ((m_ref == -kInf) ? 0.0f : m_ref) - (float)e;
-    const u32 h16 = e < 15 ? (u32)(15 - e) << 10 : 1u << (24 - e);   // fp16 2^-e, e <= 24
-    const half2_t w2 = as_half2(h16 | (h16 << 16));
+    const float wl = exp2_int(-e);   // row-sum weight of this tile's P'
     u32 pk[2][8];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -401,9 +539,9 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
       for (int r = 0; r < 16; r += 2) {
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r], scale_log2, -shift));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r + 1], scale_log2, -shift));
-        const u32 w = pack_f16x2(p0, p1);
-        pk[kb][r >> 1] = w;
-        l_run = __builtin_amdgcn_fdot2(as_half2(w), w2, l_run, false);
+        pk[kb][r >> 1] = pack_f16x2(p0, p1);
+        l_even = __builtin_fmaf(p0, wl, l_even);
+        l_odd = __builtin_fmaf(p1, wl, l_odd);
       }
     // ---- O^T += V^T P^T over the 4 key steps (16 keys each) of the tile
 #pragma unroll
@@ -429,7 +567,9 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
   // read in iteration t-1, before this iteration's barrier).  Unrolled by two so every LDS
   // address names its array.
   // The exponent of tile t+1 is loaded at the top of iteration t, ahead of that iteration's
-  // DMA: vmcnt retires in order, so a later wait on it would also wait for the DMA.
+  // DMA: vmcnt retires in order, so a later wait on it would also wait for the DMA.  Every
+  // wave reads every exponent of the block's key range, so `exact` is workgroup-uniform.
+  bool exact = false;
   if (ntiles > 0) issue(0, kbuf0, vbuf0);
   int e_cur = ntiles > 0 ? eh[0] : 0;
   for (int tile = 0; tile < ntiles;) {
@@ -438,6 +578,7 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
     int e_next = tile + 1 < ntiles ? eh[tile + 1] : 0;
     __builtin_amdgcn_sched_barrier(0);
     if (tile + 1 < ntiles) issue(tile + 1, kbuf1, vbuf1);
+    exact |= e_cur > e_max;
     body(tile, kbuf0, vbuf0, e_cur);
     e_cur = e_next;
     if (++tile >= ntiles) break;
@@ -446,27 +587,36 @@ __device__ __forceinline__ void attention_fwd(const __bf16* __restrict__ q,
     e_next = tile + 1 < ntiles ? eh[tile + 1] : 0;
     __builtin_amdgcn_sched_barrier(0);
     if (tile + 1 < ntiles) issue(tile + 1, kbuf0, vbuf0);
+    exact |= e_cur > e_max;
     body(tile, kbuf1, vbuf1, e_cur);
     e_cur = e_next;
     ++tile;
   }
+  T* orow0 = o + (i64)bh * sq * D;
+  float* lse_row0 = lse != nullptr ? lse + (i64)bh * sq : nullptr;
+  if (exact) {
+    attention_exact_rows<T, D, CAUSAL>(qp, kp, v + b * vsb + h * vsh, orow0, lse_row0, sq, sk,
+                                       q0, qss, kss, vss, scale_log2);
+    return;
+  }
   // ---- readout: O / l, and the natural-log LSE of the scaled scores
-  const float l_tot = l_run + partner<32>(l_run);
+  const float l_lane = l_even + l_odd;
+  const float l_tot = l_lane + partner<32>(l_lane);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (my_q < sq) {
-    __bf16* orow = o + ((i64)bh * sq + my_q) * D;
+    T* orow = orow0 + (i64)my_q * D;
 #pragma unroll
     for (int a = 0; a < DBLK; ++a) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         u32x2 w;
-        w.x = pack_bf16x2(oacc[a][4 * g + 0] * inv, oacc[a][4 * g + 1] * inv);
-        w.y = pack_bf16x2(oacc[a][4 * g + 2] * inv, oacc[a][4 * g + 3] * inv);
+        w.x = In::pack2(oacc[a][4 * g + 0] * inv, oacc[a][4 * g + 1] * inv);
+        w.y = In::pack2(oacc[a][4 * g + 2] * inv, oacc[a][4 * g + 3] * inv);
         *(u32x2*)(orow + a * 32 + 8 * g + 4 * hi) = w;
       }
     }
-    if (lse != nullptr && hi == 0)
-      lse[(i64)bh * sq + my_q] = (m_ref + __builtin_log2f(l_tot)) * 0.6931471805599453f;
+    if (lse_row0 != nullptr && hi == 0)
+      lse_row0[my_q] = (m_ref + __builtin_log2f(l_tot)) * 0.6931471805599453f;
   }
 }
 

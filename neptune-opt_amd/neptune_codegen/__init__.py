@@ -15,8 +15,8 @@ from neptune_codegen.algebra import (MergeCertificate, StateCertificate, _as_quo
                                      derive_merge_certificate, derive_state_certificate,
                                      reachable_producer_domain, repair_bias, repair_factor,
                                      repair_pair, term_expr, vanishes)
-from neptune_codegen.attention import (as_attention_op, attention_fold, launch_attention,
-                                       run_attention)
+from neptune_codegen.attention import (as_attention_op, attention_fold, exact_path_taken,
+                                       launch_attention, run_attention)
 from neptune_codegen.autotune import best_config, machine_key, op_key, parameter_tag
 from neptune_codegen.emitters import (check_supported, derived_producer_expr, emit_fold_policy,
                                       emit_kernel_source, emit_rms_state_source,
@@ -63,7 +63,7 @@ __all__ = [
     "as_triton_op", "as_hip_op", "op_handle", "triton_op_name", "as_state_op",
     "state_op_handle", "as_segment_op", "segment_op_handle", "run_segment_pool",
     "compile_segment_reduction", "validate_segment_inputs",
-    "run_attention", "attention_fold", "as_attention_op", "launch_attention",
+    "run_attention", "attention_fold", "as_attention_op", "launch_attention", "exact_path_taken",
     "compile_readout", "run_readout", "run_log_softmax", "as_readout_op", "readout_op_handle",
     "best_config", "machine_key", "op_key", "parameter_tag", "prebuilt_programs",
 ]

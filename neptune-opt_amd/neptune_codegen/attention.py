@@ -6,10 +6,17 @@ exp(s - s2) (tests/test_neptune_opt.py:347) applied per key tile to the running
 (max, sum, output) state, with MFMA for Q K^T and P V.  The causal mask is torch's
 `is_causal=True` (query i sees keys j <= i).  The oracle is the closed form in fp32.
 
-Layout contract: q [B, H, Sq, D], k/v [B, H, Sk, D], bf16, unit stride on D; other strides
-are honoured (rows must be 16-byte aligned, otherwise the input is made contiguous).  Output
-is a fresh contiguous [B, H, Sq, D] bf16 tensor; `return_lse` adds the fp32 [B, H, Sq]
-natural-log logsumexp of the scaled, masked scores.
+Layout contract: q [B, H, Sq, D], k/v [B, H, Sk, D], one dtype (bf16 or fp16), unit stride
+on D; other strides are honoured (rows must be 16-byte aligned, otherwise the input is made
+contiguous).  Output is a fresh contiguous [B, H, Sq, D] tensor of the input dtype;
+`return_lse` adds the fp32 [B, H, Sq] natural-log logsumexp of the scaled, masked scores.
+
+Every input has a result; nothing is refused at run time and no device-side assert is used.
+The MFMA path feeds V to the P.V product as fp16 images scaled per 64-key tile by a power of
+two (exact for |v| < 2^28 in a tile, see V_EXPONENT_MAX).  A workgroup whose keys include a
+tile beyond that (|v| >= 2^28, inf or NaN) recomputes its queries with the kernel's exact fp32
+path: O = sum_j p_j v_j / sum_j p_j over the visible keys in IEEE fp32, so only rows that see
+a non-finite V value become non-finite.
 """
 from __future__ import annotations
 
@@ -29,21 +36,19 @@ BLOCK_N = 64            # keys per tile (one V^T image per tile)
 K_ROW_STRIDE_MAX = 1 << 24   # K rows are addressed with 32-bit byte offsets within a tile
 # V^T tiles are fp16 images of v * 2^-e, e the tile's exponent (0 below 2^15).  A tile value
 # below 2^(e - 14) keeps only an absolute precision of 2^(e - 25), which bounds the error it
-# adds to O; e <= 13 keeps that under 2^-12, a quarter of the bf16 absolute tolerance.  Larger
-# tiles, and inf/NaN, are refused.  (fp32 accumulation of O, |O acc| <= keys * 2^8 * 2^28,
-# cannot overflow at this bound.)
+# adds to O; e <= 13 keeps that under 2^-12, a quarter of the bf16 absolute tolerance.  Blocks
+# of queries that see a larger tile, or inf/NaN in V, take the exact fp32 path.  (fp32
+# accumulation of O, |O acc| <= keys * 2^8 * 2^28, cannot overflow at this bound.)
 V_EXPONENT_MAX = 13
-V_RANGE_MESSAGE = ("attention fold: V must be finite with |v| < 2^28 (a larger value would take "
-                   "the fp16 precision of the other values of its 64-key tile)")
 
 
-def _program(head_dim: int, causal: bool) -> hip.Program:
-    key = (head_dim, causal)
+def _program(head_dim: int, causal: bool, dtype="bfloat16") -> hip.Program:
+    key = (head_dim, causal, str(dtype))
     with _lock:
         prog = _PROGRAMS.get(key)
         if prog is None:
-            prog = hip.Program(emit_attention_source(head_dim, causal),
-                               f"{attention_kernel_name(head_dim, causal)}.hip", BASE_OPTIONS)
+            prog = hip.Program(emit_attention_source(head_dim, causal, dtype),
+                               f"{attention_kernel_name(head_dim, causal, dtype)}.hip", BASE_OPTIONS)
             _PROGRAMS[key] = prog
         return prog
 
@@ -56,12 +61,14 @@ def validate_attention_inputs(q, k, v, *, metadata: bool = False):
             raise TypeError(f"attention {nm} must be strided")
         if t.ndim != 4:
             raise ValueError(f"attention {nm} must be [batch, heads, seq, head_dim]")
-        if t.dtype != torch.bfloat16:
-            raise TypeError(f"attention fold supports bfloat16 inputs, got {t.dtype} for {nm}")
+        if t.dtype not in (torch.bfloat16, torch.float16):
+            raise TypeError(f"attention fold supports bfloat16 and float16 inputs, got {t.dtype} for {nm}")
         if not metadata and t.device.type != "cuda":
             raise ValueError("attention execution requires a ROCm (cuda) device")
     if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
         raise ValueError(f"attention shapes do not match: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError(f"attention q, k, v must share one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
     if q.device != k.device or q.device != v.device:
         raise ValueError("attention tensors must be on the same device")
     if q.shape[3] not in (64, 128):
@@ -78,22 +85,22 @@ def _kernel_ready(t):
 
 def run_attention(q, k, v, *, scale: float | None = None, causal: bool = True,
                   return_lse: bool = False):
-    """Attention fold on the current stream; see the module docstring for the contract.  V
-    holding inf/NaN or |v| >= 2^28 is refused by a device-side assert (V_RANGE_MESSAGE),
-    raised at the next synchronisation."""
-    import torch
-
-    out, lse, status = launch_attention(q, k, v, scale=scale, causal=causal, return_lse=return_lse)
-    if status is not None:
-        torch._assert_async(status, V_RANGE_MESSAGE)
+    """Attention fold on the current stream; see the module docstring for the contract."""
+    out, lse, _ = launch_attention(q, k, v, scale=scale, causal=causal, return_lse=return_lse)
     return (out, lse) if return_lse else out
 
 
 def launch_attention(q, k, v, *, scale: float | None = None, causal: bool = True,
                      return_lse: bool = False):
-    """(out, lse or None, status or None): the fold's launches without the range assert.
-    `status` is one int32 on the device, 1 when every V tile was in range and 0 otherwise
-    (None when nothing was launched)."""
+    """(out, lse or None, exps or None): the fold's two launches.  `exps` is the int32 tile
+    exponent table [B*H*ceil(Sk/64)] the V^T pack wrote (None when nothing was launched);
+    `exact_path_taken(exps)` tells whether some query block took the exact fp32 path."""
+    return _launch(q, k, v, scale, causal, return_lse, V_EXPONENT_MAX)
+
+
+def _launch(q, k, v, scale, causal, return_lse, e_max: int):
+    """The launches with the exact path's threshold as a parameter: e_max = -1 sends every
+    query block through the exact fp32 path (the tests compare the two paths with it)."""
     import torch
     from torch._subclasses.fake_tensor import FakeTensor
 
@@ -116,25 +123,29 @@ def launch_attention(q, k, v, *, scale: float | None = None, causal: bool = True
     # V^T tile images (fp16, MFMA operand order) and one power-of-two exponent per tile
     vt = torch.empty((B * H * ntiles * D * BLOCK_N,), dtype=torch.float16, device=q.device)
     exps = torch.empty((B * H * ntiles,), dtype=torch.int32, device=q.device)
-    prog = _program(D, causal)
-    pack = prog.kernel(attention_pack_kernel_name(D),
-                       (hip.PTR,) * 4 + (hip.I32,) * 3 + (hip.I64,) * 3, 256, device)
-    fold = prog.kernel(attention_kernel_name(D, causal),
-                       (hip.PTR,) * 6 + (hip.I32,) * 3 + (hip.I64,) * 6 + (hip.F32,),
+    prog = _program(D, causal, q.dtype)
+    pack = prog.kernel(attention_pack_kernel_name(D, q.dtype),
+                       (hip.PTR,) * 3 + (hip.I32,) * 2 + (hip.I64,) * 3, 256, device)
+    fold = prog.kernel(attention_kernel_name(D, causal, q.dtype),
+                       (hip.PTR,) * 7 + (hip.I32,) * 3 + (hip.I64,) * 9 + (hip.I32, hip.F32),
                        ATTN_FOLD_THREADS, device)
     stream = hip.current_stream(q.device)
-    # one status word: set here, cleared by the pack kernel for a V tile out of range
-    status = torch.ones(1, dtype=torch.int32, device=q.device)
     pack.launch((B * H * ntiles,),
-                (v.data_ptr(), vt.data_ptr(), exps.data_ptr(), status.data_ptr(),
-                 V_EXPONENT_MAX, H, Sk, v.stride(0), v.stride(1), v.stride(2)), stream)
+                (v.data_ptr(), vt.data_ptr(), exps.data_ptr(), H, Sk,
+                 v.stride(0), v.stride(1), v.stride(2)), stream)
     nqb = (Sq + BLOCK_M - 1) // BLOCK_M
     fold.launch((nqb * B * H,),
-                (q.data_ptr(), k.data_ptr(), vt.data_ptr(), exps.data_ptr(), out.data_ptr(),
-                 lse.data_ptr() if lse is not None else 0, H, Sq, Sk,
+                (q.data_ptr(), k.data_ptr(), vt.data_ptr(), exps.data_ptr(), v.data_ptr(),
+                 out.data_ptr(), lse.data_ptr() if lse is not None else 0, H, Sq, Sk,
                  q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
-                 scale * LOG2E), stream)
-    return out, lse, status
+                 v.stride(0), v.stride(1), v.stride(2), int(e_max), scale * LOG2E), stream)
+    return out, lse, exps
+
+
+def exact_path_taken(exps) -> bool:
+    """Host check (synchronises): some V tile was beyond the MFMA path's range, so the query
+    blocks that see it were computed by the exact fp32 path."""
+    return bool((exps > V_EXPONENT_MAX).any().item())
 
 
 attention_fold = run_attention

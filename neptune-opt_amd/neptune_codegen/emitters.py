@@ -526,36 +526,50 @@ ATTN_WAVES_PER_EU = 2
 ATTN_FOLD_THREADS = 512
 
 
-def emit_attention_source(head_dim: int, causal: bool, waves_per_eu: int | None = None) -> str:
+ATTN_DTYPES = {"bfloat16": ("bf16", "__bf16"), "float16": ("f16", "_Float16")}
+
+
+def _attn_dtype(dtype) -> tuple[str, str]:
+    key = str(dtype).replace("torch.", "")
+    if key not in ATTN_DTYPES:
+        raise TypeError(f"attention fold supports bfloat16 and float16 inputs, got {dtype}")
+    return ATTN_DTYPES[key]
+
+
+def emit_attention_source(head_dim: int, causal: bool, dtype="bfloat16",
+                          waves_per_eu: int | None = None) -> str:
     """hiprtc unit of the online-softmax attention fold (no reference counterpart): the
     logsumexp repair exp(s - s2) applied per key tile to (m, l, O).  Holds two kernels: the
-    V^T tile packer and the fold itself."""
+    V^T tile packer and the fold itself (with its exact fallback for out-of-range V)."""
     wpe = ATTN_WAVES_PER_EU if waves_per_eu is None else waves_per_eu
     if head_dim not in (64, 128):
         raise NotImplementedError("attention fold supports head_dim 64 and 128")
-    name = attention_kernel_name(head_dim, causal)
-    pack = attention_pack_kernel_name(head_dim)
+    tag, ctype = _attn_dtype(dtype)
+    name = attention_kernel_name(head_dim, causal, dtype)
+    pack = attention_pack_kernel_name(head_dim, dtype)
     return "\n".join([
         "// AUTO-GENERATED by neptune_codegen (HIP emitter) -- do not edit.\n"
-        f"// online-softmax attention fold: head_dim={head_dim}, causal={causal}; bf16 MFMA for "
-        "Q K^T, fp16 MFMA for P V, fp32 running max/sum.\n",
+        f"// online-softmax attention fold: head_dim={head_dim}, causal={causal}, {tag} inputs; "
+        f"{tag} MFMA for Q K^T, fp16 MFMA for P V, fp32 running max/sum.\n",
         kernel_header("nep_device.h", "nep_attention.h"),
         f'extern "C" __global__ void __launch_bounds__(256) {pack}(const void* v, void* vt, int* exps, '
-        "int* status, int e_max, int heads, int sk, long long vsb, long long vsh, long long vss) {\n"
-        f"  nep::attention_vt_pack<{head_dim}>((const __bf16*)v, (nep::u16*)vt, exps, status, e_max, "
+        "int heads, int sk, long long vsb, long long vsh, long long vss) {\n"
+        f"  nep::attention_vt_pack<{ctype}, {head_dim}>((const {ctype}*)v, (nep::u16*)vt, exps, "
         "heads, sk, vsb, vsh, vss);\n}\n",
         f'extern "C" __global__ void __launch_bounds__({ATTN_FOLD_THREADS}, {wpe}) {name}(const void* q, const void* k, '
-        "const void* vt, const int* exps, void* o, float* lse, int heads, int sq, int sk, "
-        "long long qsb, long long qsh, long long qss, long long ksb, long long ksh, long long kss, "
-        "float scale_log2) {\n"
-        f"  nep::attention_fwd<{head_dim}, {'true' if causal else 'false'}>((const __bf16*)q, "
-        "(const __bf16*)k, (const nep::u16*)vt, exps, (__bf16*)o, lse, heads, sq, sk, qsb, qsh, qss, "
-        "ksb, ksh, kss, scale_log2);\n}\n"])
+        "const void* vt, const int* exps, const void* v, void* o, float* lse, int heads, int sq, "
+        "int sk, long long qsb, long long qsh, long long qss, long long ksb, long long ksh, "
+        "long long kss, long long vsb, long long vsh, long long vss, int e_max, float scale_log2) {\n"
+        f"  nep::attention_fwd<{ctype}, {head_dim}, {'true' if causal else 'false'}>((const {ctype}*)q, "
+        f"(const {ctype}*)k, (const nep::u16*)vt, exps, (const {ctype}*)v, ({ctype}*)o, lse, heads, "
+        "sq, sk, qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss, e_max, scale_log2);\n}\n"])
 
 
-def attention_kernel_name(head_dim: int, causal: bool) -> str:
-    return f"attention_fold_d{head_dim}_{'causal' if causal else 'full'}"
+def attention_kernel_name(head_dim: int, causal: bool, dtype="bfloat16") -> str:
+    tag, _ = _attn_dtype(dtype)
+    return f"attention_fold_{tag}_d{head_dim}_{'causal' if causal else 'full'}"
 
 
-def attention_pack_kernel_name(head_dim: int) -> str:
-    return f"attention_vt_pack_d{head_dim}"
+def attention_pack_kernel_name(head_dim: int, dtype="bfloat16") -> str:
+    tag, _ = _attn_dtype(dtype)
+    return f"attention_vt_pack_{tag}_d{head_dim}"

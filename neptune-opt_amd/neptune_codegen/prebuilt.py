@@ -74,7 +74,8 @@ def _segment_programs():
 def _attention_programs():
     from neptune_codegen.attention import _program
 
-    return [_program(128, True), _program(128, False), _program(64, True)]
+    return [_program(128, True), _program(128, False), _program(64, True), _program(64, False),
+            _program(128, True, "float16"), _program(64, False, "float16")]
 
 
 def programs():

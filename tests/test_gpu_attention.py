@@ -1,7 +1,8 @@
 """GPU parity of the online-softmax attention fold against the fp32 closed form.
 
-Tolerance: bf16 rtol 1.6e-2 / atol 1e-3, against
-softmax(scale * Q K^T + torch is_causal mask) V computed in fp32 on the CPU.
+Tolerance: bf16/fp16 rtol 1.6e-2 / atol 1e-3 for O, against
+softmax(scale * Q K^T + torch is_causal mask) V computed in fp32 on the CPU; fp32 rtol 1e-5 /
+atol 1e-6 for the logsumexp side output against torch.logsumexp of the same fp32 scores.
 """
 import math
 
@@ -9,17 +10,15 @@ import pytest
 import torch
 
 import neptune_codegen as CG
+from neptune_codegen import attention as A
 from neptune_codegen import hip
 from neptune_codegen.emitters import BASE_OPTIONS, kernel_header
 from oracle import references as R
 
 pytestmark = pytest.mark.gpu
-# The fold's row sum l adds the fp16-rounded P values that the P.V MFMA multiplies (so O is
-# normalised by exactly the weights it used).  A normal fp16 rounding errs by at most 2^-11
-# relative (fp16's unit roundoff); a subnormal one (P < 2^-14) by at most 2^-25 absolute.  The
-# row's largest P is >= 1, so l >= 1, and for at most 4096 keys the logsumexp m + log(l) is
-# within -log(1 - 2^-11) + 4096 * 2^-25 (+ fp32 rounding of m + log l) of the fp32 value.
-LSE_ATOL = -math.log1p(-2.0 ** -11) + 4096 * 2.0 ** -25 + 1e-6
+# The row sum l adds the fp32 P values, so the logsumexp side output is an fp32 result:
+# BASELINE.json's fp32 tolerance applies.
+LSE_RTOL, LSE_ATOL = 1e-5, 1e-6
 
 
 def _dev():
@@ -60,10 +59,22 @@ extern "C" __global__ void mfma_probe(const __bf16* a, const __bf16* b, float* c
     torch.testing.assert_close(c.cpu(), a.float() @ b.float(), rtol=0, atol=0)
 
 
+def _lse_reference(q, k, causal, scale=None):
+    Sq, Sk, D = q.shape[2], k.shape[2], q.shape[3]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    s = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) * scale
+    if causal:
+        s = s.masked_fill(~torch.ones(Sq, Sk, dtype=torch.bool).tril(0), float("-inf"))
+    return torch.logsumexp(s, -1)
+
+
+SHAPES = [(1, 2, 256, 256, 128), (2, 3, 200, 200, 128), (1, 1, 77, 77, 128),
+          (1, 2, 130, 333, 64), (1, 1, 1, 64, 128), (1, 4, 512, 512, 64),
+          (1, 2, 333, 130, 128), (2, 1, 700, 65, 64)]
+
+
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("shape", [(1, 2, 256, 256, 128), (2, 3, 200, 200, 128), (1, 1, 77, 77, 128),
-                                   (1, 2, 130, 333, 64), (1, 1, 1, 64, 128), (1, 4, 512, 512, 64),
-                                   (1, 2, 333, 130, 128), (2, 1, 700, 65, 64)])
+@pytest.mark.parametrize("shape", SHAPES)
 def test_attention_parity(shape, causal):
     dev = _dev()
     B, H, Sq, Sk, D = shape
@@ -75,10 +86,64 @@ def test_attention_parity(shape, causal):
     got, lse = CG.run_attention(q.to(dev), k.to(dev), v.to(dev), causal=causal, return_lse=True)
     want = R.attention_reference(q, k, v, causal=causal)
     torch.testing.assert_close(got.cpu().float(), want.float(), rtol=1.6e-2, atol=1e-3)
-    s = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) / math.sqrt(D)
-    if causal:
-        s = s.masked_fill(~torch.ones(Sq, Sk, dtype=torch.bool).tril(0), float("-inf"))
-    torch.testing.assert_close(lse.cpu(), torch.logsumexp(s, -1), rtol=1e-5, atol=LSE_ATOL)
+    torch.testing.assert_close(lse.cpu(), _lse_reference(q, k, causal), rtol=LSE_RTOL, atol=LSE_ATOL)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(1, 2, 256, 256, 128), (2, 3, 200, 200, 128), (1, 2, 130, 333, 64),
+                                   (1, 1, 1, 64, 128), (2, 1, 700, 65, 64)])
+def test_attention_parity_fp16(shape, causal):
+    """fp16 Q/K/V: the f16 MFMA for Q K^T, the same fp16 P.V, an fp16 output."""
+    dev = _dev()
+    B, H, Sq, Sk, D = shape
+    g = torch.Generator().manual_seed(15)
+    q = torch.randn(B, H, Sq, D, generator=g).half()
+    k = torch.randn(B, H, Sk, D, generator=g).half()
+    v = (3 * torch.randn(B, H, Sk, D, generator=g)).half()
+    _say(f"attention fp16 {shape} causal={causal}")
+    got, lse = CG.run_attention(q.to(dev), k.to(dev), v.to(dev), causal=causal, return_lse=True)
+    assert got.dtype == torch.float16
+    want = R.attention_reference(q, k, v, causal=causal)
+    torch.testing.assert_close(got.cpu().float(), want.float(), rtol=1.6e-2, atol=1e-3)
+    torch.testing.assert_close(lse.cpu(), _lse_reference(q, k, causal), rtol=LSE_RTOL, atol=LSE_ATOL)
+
+
+def test_attention_fp16_values_at_the_top_of_the_range():
+    """fp16 V holding 65504 and -32768 (tile exponent 1) next to fp16 subnormals."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(16)
+    B, H, S, D = 1, 2, 200, 128
+    q, k = (torch.randn(B, H, S, D, generator=g).half() for _ in range(2))
+    v = torch.randn(B, H, S, D, generator=g)
+    v[0, 0, 10, 5] = 65504.0
+    v[0, 1, 150, 0] = -32768.0
+    v[0, 1, 151, 1:9] = 2.0 ** -20
+    v = v.half()
+    _say("attention fp16 top-of-range V")
+    out, _, exps = CG.launch_attention(q.to(dev), k.to(dev), v.to(dev), causal=True)
+    assert not CG.exact_path_taken(exps)
+    torch.testing.assert_close(out.cpu().float(), R.attention_reference(q, k, v, causal=True).float(),
+                               rtol=1.6e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(1, 2, 256, 256, 128), (1, 1, 300, 333, 64), (2, 1, 77, 77, 128)])
+def test_attention_exact_path_matches_the_fp32_closed_form(shape, causal, dtype):
+    """The exact fp32 path (forced for every query block by an exponent threshold of -1): fp32
+    scores, fp32 P, the caller's V.  Its O is within the storage rounding of the fp32 closed
+    form, and its logsumexp within the fp32 tolerance."""
+    dev = _dev()
+    B, H, Sq, Sk, D = shape
+    g = torch.Generator().manual_seed(17)
+    q, k, v = (torch.randn(B, H, n, D, generator=g).to(dtype) for n in (Sq, Sk, Sk))
+    _say(f"attention exact path {shape} causal={causal} {dtype}")
+    out, lse, _ = A._launch(q.to(dev), k.to(dev), v.to(dev), None, causal, True, -1)
+    want = R.attention_reference(q.float(), k.float(), v.float(), causal=causal)
+    # one rounding of an fp32 value: half an ulp, 2^-8 (bf16) or 2^-11 (fp16) relative at most
+    half_ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    torch.testing.assert_close(out.cpu().float(), want, rtol=1.01 * half_ulp, atol=1e-5)
+    torch.testing.assert_close(lse.cpu(), _lse_reference(q, k, causal), rtol=LSE_RTOL, atol=LSE_ATOL)
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -107,11 +172,11 @@ def test_attention_large_values_use_scaled_tiles(causal):
 
 @pytest.mark.parametrize("causal", [True, False])
 def test_attention_largest_accepted_v_tile_next_to_masked_and_normal_keys(causal):
-    """Tiles holding |v| just below 2^28 (tile exponent 13, the largest accepted): packed as
-    v * 2^-13, fed P * 2^13 with a row-sum weight of 2^-13, the reference max held 6 higher.
-    The tile's other values keep 2^-12 absolute precision -- also on causal rows that see the
-    tile but not its large key (queries 64-99 for the key at 100) -- and later tiles' P stay
-    within fp16's normal range down to 2^-8 of their unlifted value."""
+    """Tiles holding |v| just below 2^28 (tile exponent 13, the largest the MFMA path takes):
+    packed as v * 2^-13, fed P * 2^13 with a row-sum weight of 2^-13, the reference max held 6
+    higher.  The tile's other values keep 2^-12 absolute precision -- also on causal rows that
+    see the tile but not its large key (queries 64-99 for the key at 100) -- and later tiles'
+    P stay within fp16's normal range down to 2^-8 of their unlifted value."""
     dev = _dev()
     g = torch.Generator().manual_seed(13)
     B, H, S, D = 1, 1, 400, 128
@@ -122,27 +187,77 @@ def test_attention_largest_accepted_v_tile_next_to_masked_and_normal_keys(causal
     v[0, 0, 5, 9] = -2.0 ** 27                        # tile 0, another exponent-13 tile
     v = v.bfloat16()
     _say(f"attention exponent-13 V tiles causal={causal}")
-    out, lse, status = CG.launch_attention(q.to(dev), k.to(dev), v.to(dev), causal=causal)
-    assert status.item() == 1
+    out, lse, exps = CG.launch_attention(q.to(dev), k.to(dev), v.to(dev), causal=causal,
+                                         return_lse=True)
+    assert not CG.exact_path_taken(exps)
+    assert exps.cpu().tolist()[:2] == [13, 13]
     want = R.attention_reference(q, k, v, causal=causal).float()
     got = out.cpu().float()
     assert torch.isfinite(got).all()
     torch.testing.assert_close(got, want, rtol=1.6e-2, atol=1e-3)
+    torch.testing.assert_close(lse.cpu(), _lse_reference(q, k, causal), rtol=LSE_RTOL, atol=LSE_ATOL)
 
 
-def test_attention_refuses_v_out_of_range_through_its_status_word():
-    """|v| >= 2^28 or inf/NaN in V clear the status word that run_attention asserts on (read
-    back here instead, so no device-side assert fires); in-range inputs leave it set."""
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("value", [2.0 ** 28, -(2.0 ** 40), 2.0 ** 100, 3.0e38])
+def test_attention_large_finite_v_takes_the_exact_path(value, causal):
+    """|v| >= 2^28 is beyond the fp16 images' range: the pack records the tile's own exponent
+    and the query blocks that see the tile take the exact fp32 path.  Rows before the tile
+    (causal) stay on the MFMA path; every row matches the fp32 closed form."""
     dev = _dev()
     g = torch.Generator().manual_seed(14)
-    q, k, v = (torch.randn(1, 2, 200, 64, generator=g).bfloat16() for _ in range(3))
-    for value, expected in ((2.0 ** 27, 1), (2.0 ** 28, 0), (2.0 ** 40, 0), (float("inf"), 0),
-                            (float("nan"), 0), (-(2.0 ** 100), 0)):
-        bad = v.clone()
-        bad[0, 1, 150, 7] = value
-        _say(f"attention V range status, v={value}")
-        _, _, status = CG.launch_attention(q.to(dev), k.to(dev), bad.to(dev), causal=True)
-        assert status.item() == expected, value
+    B, H, S, D = 1, 2, 600, 64
+    q, k = (torch.randn(B, H, S, D, generator=g).bfloat16() for _ in range(2))
+    v = torch.randn(B, H, S, D, generator=g)
+    v[0, 1, 450, 7] = value
+    v[0, 1, 452, 2] = 1e-3
+    v = v.bfloat16()
+    _say(f"attention large V {value} causal={causal}")
+    out, lse, exps = CG.launch_attention(q.to(dev), k.to(dev), v.to(dev), causal=causal,
+                                         return_lse=True)
+    e = exps.view(B * H, -1).cpu()
+    assert int(e[1, 450 // 64]) == int(math.floor(math.log2(abs(float(torch.tensor(value).bfloat16()))))) - 14
+    assert CG.exact_path_taken(exps)
+    want = R.attention_reference(q, k, v, causal=causal).float()
+    got = out.cpu().float()
+    assert torch.isfinite(got).all()
+    torch.testing.assert_close(got, want, rtol=1.6e-2, atol=1e-3)
+    torch.testing.assert_close(lse.cpu(), _lse_reference(q, k, causal), rtol=LSE_RTOL, atol=LSE_ATOL)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("value", [float("inf"), float("-inf"), float("nan")])
+def test_attention_non_finite_v_reaches_only_the_rows_that_see_it(value, causal):
+    """inf/NaN in V: no error and no trap.  The query blocks that see the tile take the exact
+    fp32 path, where masked keys contribute nothing: the rows that see the key get inf/NaN in
+    its column (p > 0 times the value), every other value matches the fp32 closed form of the
+    keys the row sees."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(18)
+    B, H, S, D = 1, 2, 700, 128
+    j, col = 530, 9
+    q, k = (torch.randn(B, H, S, D, generator=g).bfloat16() for _ in range(2))
+    v = torch.randn(B, H, S, D, generator=g).bfloat16()
+    v[0, 0, j, col] = value
+    _say(f"attention non-finite V {value} causal={causal}")
+    out, lse, exps = CG.launch_attention(q.to(dev), k.to(dev), v.to(dev), causal=causal,
+                                         return_lse=True)
+    assert CG.exact_path_taken(exps)
+    got = out.cpu().float()
+    clean = v.clone()
+    clean[0, 0, j, col] = 0.0
+    want = R.attention_reference(q, k, clean, causal=causal).float()
+    sees = torch.zeros(S, dtype=torch.bool)
+    sees[j if causal else 0:] = True
+    bad = got[0, 0, :, col]
+    if math.isnan(value):
+        assert torch.isnan(bad[sees]).all()
+    else:
+        assert (bad[sees] == value).all()
+    keep = torch.ones_like(got, dtype=torch.bool)
+    keep[0, 0, sees, col] = False
+    torch.testing.assert_close(got[keep], want[keep], rtol=1.6e-2, atol=1e-3)
+    torch.testing.assert_close(lse.cpu(), _lse_reference(q, k, causal), rtol=LSE_RTOL, atol=LSE_ATOL)
 
 
 def test_attention_strided_layout_and_scale():

@@ -23,12 +23,9 @@ import neptune_codegen as CG
 from oracle import references as R
 
 pytestmark = pytest.mark.gpu
-# The fold's row sum l adds the fp16-rounded P values that the P.V MFMA multiplies (so O is
-# normalised by exactly the weights it used).  A normal fp16 rounding errs by at most 2^-11
-# relative (fp16's unit roundoff); a subnormal one (P < 2^-14) by at most 2^-25 absolute.  The
-# row's largest P is >= 1, so l >= 1, and for at most 4096 keys the logsumexp m + log(l) is
-# within -log(1 - 2^-11) + 4096 * 2^-25 (+ fp32 rounding of m + log l) of the fp32 value.
-LSE_ATOL = -math.log1p(-2.0 ** -11) + 4096 * 2.0 ** -25 + 1e-6
+# The attention fold's row sum adds the fp32 P values: its logsumexp side output is an fp32
+# result, held to BASELINE.json's fp32 tolerance.
+LSE_RTOL, LSE_ATOL = 1e-5, 1e-6
 
 
 def _dev():
@@ -134,5 +131,5 @@ def test_cfg5_sixteen_heads_every_query_block():
         torch.testing.assert_close(out[b:b + 1, h:h + 1].float(), want, rtol=1.6e-2, atol=1e-3)
         s = torch.matmul(qs.float(), ks.float().transpose(-1, -2).contiguous()) / math.sqrt(D)
         s = s.masked_fill(~mask, float("-inf"))
-        torch.testing.assert_close(lse[b:b + 1, h:h + 1], torch.logsumexp(s, -1), rtol=1e-5, atol=LSE_ATOL)
+        torch.testing.assert_close(lse[b:b + 1, h:h + 1], torch.logsumexp(s, -1), rtol=LSE_RTOL, atol=LSE_ATOL)
     assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
