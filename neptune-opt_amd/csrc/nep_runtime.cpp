@@ -318,17 +318,43 @@ int check_split(const char* who, uint64_t partial_kernel, uint64_t merge_kernel,
   if (nparts > kMaxSplitParts) return bad("nparts exceeds the split capacity of 4096 partials");
   if (partial_threads == 0 || partial_threads > 1024 || partial_threads % 64 != 0)
     return bad("partial_threads must be a multiple of 64 in [64, 1024]");
+  // Any value only sizes the grid: the partial kernel strides over the virtual rows.
   if (parts_per_workgroup == 0 || parts_per_workgroup > partial_threads)
     return bad("parts_per_workgroup must be in [1, partial_threads]");
   if (rows > (int64_t(1) << 40) / nparts) return bad("rows * nparts is too large");
   return NEP_OK;
 }
 
-int run_split(uint64_t partial_kernel, uint64_t merge_kernel, const void* x, void* out,
-              int64_t rows, int64_t ncols, int64_t row_stride, int64_t col_stride, int64_t nparts,
-              int64_t block, uint32_t partial_threads, uint32_t parts_per_workgroup,
-              void* scratch_base, void* stream) {
+// The partial kernel's lane mapping is compiled for its launch bound, and the merge kernel
+// runs 256-lane workgroups: both bounds are read from the kernels themselves (after the
+// argument checks, and only when there is work to launch).
+int check_split_kernels(const char* who, uint64_t partial_kernel, uint64_t merge_kernel,
+                        uint32_t partial_threads) {
+  int bound = 0;
+  hipError_t err = hipFuncGetAttribute(&bound, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
+                                       reinterpret_cast<hipFunction_t>(partial_kernel));
+  if (err != hipSuccess) return hip_fail(err, "hipFuncGetAttribute(split partial)");
+  if (static_cast<int64_t>(partial_threads) != bound)
+    return fail(NEP_ERR_INVALID, std::string(who) + ": partial_threads " +
+                                     std::to_string(partial_threads) +
+                                     " differs from the partial kernel's workgroup size " +
+                                     std::to_string(bound));
+  err = hipFuncGetAttribute(&bound, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
+                            reinterpret_cast<hipFunction_t>(merge_kernel));
+  if (err != hipSuccess) return hip_fail(err, "hipFuncGetAttribute(split merge)");
+  if (bound < static_cast<int>(64 * kMergeRowsPerWorkgroup))
+    return fail(NEP_ERR_INVALID,
+                std::string(who) + ": the merge kernel's workgroup bound is below 256 lanes");
+  return NEP_OK;
+}
+
+int run_split(const char* who, uint64_t partial_kernel, uint64_t merge_kernel, const void* x,
+              void* out, int64_t rows, int64_t ncols, int64_t row_stride, int64_t col_stride,
+              int64_t nparts, int64_t block, uint32_t partial_threads,
+              uint32_t parts_per_workgroup, void* scratch_base, void* stream) {
   if (rows == 0) return NEP_OK;
+  int krc = check_split_kernels(who, partial_kernel, merge_kernel, partial_threads);
+  if (krc != NEP_OK) return krc;
   const int64_t count = rows * nparts;
   char* base = static_cast<char*>(scratch_base);
   float* pm = reinterpret_cast<float*>(base);
@@ -369,8 +395,9 @@ int nep_fold_split(uint64_t partial_kernel, uint64_t merge_kernel, const void* x
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(NEP_ERR_INVALID, "nep_fold_split: workspace holds " + std::to_string(workspace_bytes) +
                                      " bytes, the split needs " + std::to_string(need));
-  return run_split(partial_kernel, merge_kernel, x, out, rows, ncols, row_stride, col_stride,
-                   nparts, block, partial_threads, parts_per_workgroup, workspace, stream);
+  return run_split("nep_fold_split", partial_kernel, merge_kernel, x, out, rows, ncols,
+                   row_stride, col_stride, nparts, block, partial_threads, parts_per_workgroup,
+                   workspace, stream);
 }
 
 }  // extern "C"
@@ -434,8 +461,9 @@ int nep_fold_split_noalloc(uint64_t partial_kernel, uint64_t merge_kernel, const
   void* base = nullptr;
   rc = scratch_address(&base);
   if (rc != NEP_OK) return rc;
-  return run_split(partial_kernel, merge_kernel, x, out, rows, ncols, row_stride, col_stride,
-                   nparts, block, partial_threads, parts_per_workgroup, base, stream);
+  return run_split("nep_fold_split_noalloc", partial_kernel, merge_kernel, x, out, rows, ncols,
+                   row_stride, col_stride, nparts, block, partial_threads, parts_per_workgroup,
+                   base, stream);
 }
 
 }  // extern "C"

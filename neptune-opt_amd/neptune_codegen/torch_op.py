@@ -434,7 +434,8 @@ def _device_spans(data, segments, *, offsets, status=None):
 def _launch_segment(name, data, segments, params, plan, *, wrapper=None):
     """The segment op body.  With at least one segment and channel, the reference's span
     asserts (range, coverage unless unsafe, monotonic) are evaluated inside the fold kernel,
-    which clears a one-word status; one `_assert_async` on it follows, on the same stream.
+    which clears the device's one-word status (armed once); one `_assert_async` on it follows,
+    on the same stream.
     Otherwise the spans are built and asserted exactly as `_segment_spans` does."""
     import torch
 
@@ -446,10 +447,15 @@ def _launch_segment(name, data, segments, params, plan, *, wrapper=None):
     out = torch.empty(shape, dtype=data.dtype, device=data.device)
     nseg = shape[0]
     if type(nseg) is int and nseg > 0 and type(channels) is int and channels > 0:
-        status = torch.empty(1, dtype=torch.int32, device=data.device)
-        spans, status_set = _device_spans(data, segments, offsets=params["offsets"], status=status)
-        if not status_set:
-            status.fill_(1)
+        status = _armed_status(data.device)
+        if status is None:      # first call on this device under graph capture
+            status = torch.empty(1, dtype=torch.int32, device=data.device)
+            spans, status_set = _device_spans(data, segments, offsets=params["offsets"],
+                                              status=status)
+            if not status_set:
+                status.fill_(1)
+        else:
+            spans, _ = _device_spans(data, segments, offsets=params["offsets"])
         cover = -1 if params["offsets"] or params["unsafe"] else data.shape[0]
         flat = data.reshape(data.shape[0], channels)
         launch_segment_kernel(compile_segment_reduction(name, params, plan), flat, spans, out,
@@ -458,6 +464,29 @@ def _launch_segment(name, data, segments, params, plan, *, wrapper=None):
         return out
     _segment_spans(data, segments, offsets=params["offsets"], unsafe=params["unsafe"])
     return out
+
+
+_STATUS: dict = {}
+
+
+def _armed_status(device):
+    """The device's span-check status word: one int32 set to 1 once, outside graph capture.
+    A kernel clears it only for a malformed descriptor, and the `_assert_async` on it then
+    ends the device context, so no call needs to re-arm it.  None while capturing before the
+    word exists (the caller then arms a fresh word in the captured stream)."""
+    import torch
+
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    word = _STATUS.get(index)
+    if word is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        with _lock:
+            word = _STATUS.get(index)
+            if word is None:
+                word = torch.ones(1, dtype=torch.int32, device=torch.device("cuda", index))
+                _STATUS[index] = word
+    return word
 
 
 def launch_segment_kernel(program, flat, spans, out, *, status=None, cover=-1):

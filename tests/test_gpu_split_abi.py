@@ -35,9 +35,11 @@ def split_call(x, name="logsumexp", block=1024, **params):
     return kp, km, rows, ncols, nparts, var.wg, max(1, var.wg // var.tpr)
 
 
-def run_entry(x, block=1024, name="logsumexp", **params):
+def run_entry(x, block=1024, name="logsumexp", threads=None, ppw=None, expect_rc=0, **params):
     lib = hip.load_library()
-    kp, km, rows, ncols, nparts, threads, ppw = split_call(x, name, block, **params)
+    kp, km, rows, ncols, nparts, wg, rpw = split_call(x, name, block, **params)
+    threads = wg if threads is None else threads
+    ppw = rpw if ppw is None else ppw
     out = torch.empty(rows, dtype=x.dtype, device=x.device)
     nbytes = lib.nep_fold_split_workspace_bytes(rows, nparts)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
@@ -45,7 +47,7 @@ def run_entry(x, block=1024, name="logsumexp", **params):
                             ctypes.c_void_p(out.data_ptr()), rows, ncols, x.stride(0), x.stride(1),
                             nparts, block, threads, ppw, ctypes.c_void_p(ws.data_ptr()), nbytes,
                             ctypes.c_void_p(hip.current_stream(x.device)))
-    assert rc == 0, lib.nep_last_error()
+    assert rc == expect_rc, lib.nep_last_error()
     return out
 
 
@@ -81,3 +83,25 @@ def test_split_entry_point_strided_rows_and_another_skeleton():
     want = CG.run("stable_l2", x, plan="split", block=512)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+def test_split_entry_point_checks_threads_and_any_grid_is_exact():
+    """partial_threads is checked against the partial kernel's own workgroup size (read from
+    the kernel, NEP_ERR_INVALID on a mismatch, nothing launched); parts_per_workgroup only sizes
+    the grid, since the partial kernel strides over the (row, part) pairs: fewer or more
+    workgroups than one pass give bit-identical results."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(23)
+    x = (4 * torch.randn(48, 20000, generator=g)).bfloat16().to(dev)
+    want = CG.run("logsumexp", x, plan="split", block=1024)
+    _, _, _, _, _, wg, rpw = split_call(x, "logsumexp", 1024)
+    lib = hip.load_library()
+    for threads in {64, 128, 256, 512, 1024} - {wg}:
+        print(f"nep_fold_split refuses partial_threads={threads} (kernel: {wg})", flush=True)
+        run_entry(x, 1024, threads=threads, expect_rc=1)
+        assert "workgroup size" in lib.nep_last_error().decode()
+    for ppw in sorted({1, max(1, rpw // 2), rpw, min(wg, 2 * rpw), min(wg, 8 * rpw)}):
+        print(f"nep_fold_split parts_per_workgroup={ppw} (kernel: {rpw})", flush=True)
+        got = run_entry(x, 1024, ppw=ppw)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(got), _bits(want)), ppw

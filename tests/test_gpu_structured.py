@@ -258,3 +258,38 @@ def test_lengths_prefix_sum_kernel_is_exact(dtype):
         want = torch.cat([torch.zeros(1, dtype=torch.int64), lengths.to(torch.int64).cumsum(0)])
         assert got.dtype == torch.int64 and torch.equal(got.cpu(), want)
         assert status_set and status.item() == 1, "the first spans launch sets the status word"
+
+
+def test_segment_status_word_is_armed_once_and_graph_capture_before_it_exists():
+    """The segment op's span-check status word is armed once per device, outside capture.  A
+    first call under graph capture (no word yet) arms a word of its own in the captured
+    stream; replays and later eager calls give the reference results and leave the device
+    word set."""
+    from neptune_codegen import torch_op as TO
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(21)
+    data = torch.randn(300, 128, generator=g).half()
+    lengths = torch.tensor([0, 5, 120, 0, 75, 100], dtype=torch.int32)
+    want = R.segment_reference(data, lengths, "sum")
+    d_dev, l_dev = data.to(dev), lengths.to(dev)
+    TO._STATUS.pop(0, None)
+    _say("segment op: first call under graph capture")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            out = CG.run_segment_pool(d_dev, l_dev, reduce="sum")
+    torch.cuda.current_stream().wait_stream(s)
+    assert 0 not in TO._STATUS
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        _bits_equal(out.cpu(), want)
+    _say("segment op: eager calls arm the device word")
+    for reduce in ("sum", "mean", "sum"):
+        got = CG.run_segment_pool(d_dev, l_dev, reduce=reduce)
+        _bits_equal(got.cpu(), R.segment_reference(data, lengths, reduce))
+    assert TO._STATUS[0].item() == 1
