@@ -121,13 +121,12 @@ size_t nep_fold_split_workspace_bytes(int64_t rows, int64_t nparts);
  * generated unit's "<name>_partial_<variant>" and "<name>_merge_<dtype>" kernels
  * (nep_get_kernel); x is [rows, ncols] with strides (row_stride, col_stride) in elements, out
  * holds `rows` results in x's dtype.  nparts must be ceil(ncols / block) (block a power of
- * two, nparts <= 4096: split_launch_shape, template.py:114-125).  partial_threads must equal
- * the partial kernel's workgroup size (its __launch_bounds__, read back with
- * hipFuncGetAttribute; a mismatch fails with NEP_ERR_INVALID).  parts_per_workgroup only sizes
- * the partial grid, ceil(rows * nparts / parts_per_workgroup): the kernel strides over the
- * (row, part) pairs, so every value in [1, partial_threads] gives the same results, and the
- * kernel's own pairs per workgroup (workgroup size / lanes per part) gives one pass.
- * `workspace` is device memory of at
+ * two, nparts <= 4096: split_launch_shape, template.py:114-125).  partial_threads and
+ * parts_per_workgroup are the partial kernel's workgroup size and the (row, part) pairs one
+ * workgroup covers; the generated unit records both (its __launch_bounds__, and the size of
+ * the marker symbol "<partial kernel>_parts_per_workgroup", which hipModuleGetGlobal reports),
+ * and a call whose numbers differ fails with NEP_ERR_INVALID before any launch.  partial_kernel
+ * must have been looked up through nep_get_kernel.  `workspace` is device memory of at
  * least nep_fold_split_workspace_bytes(rows, nparts) bytes, owned by the caller and not read
  * before the partial kernel writes it.  Two launches, no synchronisation, no allocation.
  */

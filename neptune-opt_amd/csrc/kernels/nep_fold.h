@@ -638,11 +638,7 @@ __device__ __forceinline__ void fold_readout(const typename St::T* __restrict__ 
 }
 
 // Split plan, partial kernel (template.py:137-148): virtual row vr = row*nparts + part covers
-// columns [part*block, min(ncols, (part+1)*block)) and writes its exact chunk state.  A
-// workgroup takes WG/TPR consecutive virtual rows per pass and strides over the grid, so any
-// grid size covers every virtual row once (the launch shape only decides the speed; the host
-// sizes the grid to one pass).  The pass count is workgroup-uniform, so the barriers of the
-// row combine are reached by every wave.
+// columns [part*block, min(ncols, (part+1)*block)) and writes its exact chunk state.
 template <class F, class St, int TPR, int UNROLL, bool VECTOR, int WG>
 __device__ __forceinline__ void fold_split_partial(const typename St::T* __restrict__ x,
                                                    float* __restrict__ pm,
@@ -655,46 +651,43 @@ __device__ __forceinline__ void fold_split_partial(const typename St::T* __restr
   __shared__ State lds_state[WG / 64];
   __shared__ LogLane lds_lane[WG / 64];
   const int t = threadIdx.x % TPR;
-  const i64 count = rows * nparts;
-  for (i64 base = (i64)blockIdx.x * RPW; base < count; base += (i64)gridDim.x * RPW) {
-    const i64 vr = base + threadIdx.x / TPR;
-    const bool live = vr < count;
-    const i64 row = live ? vr / nparts : 0;
-    const i64 part = live ? vr % nparts : 0;
-    const typename St::T* rp = x + row * stride_row;
-    const i64 c0 = part * block;
-    i64 c1 = c0 + block;
-    c1 = c1 < ncols ? c1 : ncols;
-    if (!live) c1 = c0;
-    const float n = (float)ncols;
-    State out_state;
-    if constexpr (F::kLog) {
-      LogLane s = log_row_lane<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c0, c1, t, n);
-      s = log_row_combine<F, TPR>(s, lds_lane);
-      const bool bad = s.flag != 0 || is_nan(s.acc);
-      bool any_bad;
-      if constexpr (TPR > 64) any_bad = __syncthreads_or(bad ? 1 : 0) != 0;
-      else any_bad = __builtin_amdgcn_ballot_w64(bad) != 0;
-      out_state.m = s.m;
-      out_state.acc = s.acc;
-      out_state.seen = (s.m != -kInf) ? 1 : 0;
-      out_state.status = 0;
-      if (any_bad) {
-        const State e = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c0,
-                                                                     bad ? c1 : c0, t, n,
-                                                                     lds_state);
-        if (bad) out_state = e;
-      }
-    } else {
-      out_state = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c0, c1, t, n,
-                                                               lds_state);
+  const i64 vr = (i64)blockIdx.x * RPW + threadIdx.x / TPR;
+  const bool live = vr < rows * nparts;
+  const i64 row = live ? vr / nparts : 0;
+  const i64 part = live ? vr % nparts : 0;
+  const typename St::T* rp = x + row * stride_row;
+  const i64 c0 = part * block;
+  i64 c1 = c0 + block;
+  c1 = c1 < ncols ? c1 : ncols;
+  if (!live) c1 = c0;
+  const float n = (float)ncols;
+  State out_state;
+  if constexpr (F::kLog) {
+    LogLane s = log_row_lane<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c0, c1, t, n);
+    s = log_row_combine<F, TPR>(s, lds_lane);
+    const bool bad = s.flag != 0 || is_nan(s.acc);
+    bool any_bad;
+    if constexpr (TPR > 64) any_bad = __syncthreads_or(bad ? 1 : 0) != 0;
+    else any_bad = __builtin_amdgcn_ballot_w64(bad) != 0;
+    out_state.m = s.m;
+    out_state.acc = s.acc;
+    out_state.seen = (s.m != -kInf) ? 1 : 0;
+    out_state.status = 0;
+    if (any_bad) {
+      const State e = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c0,
+                                                                   bad ? c1 : c0, t, n,
+                                                                   lds_state);
+      if (bad) out_state = e;
     }
-    if (live && t == 0) {
-      pm[vr] = out_state.m;
-      pa[vr] = out_state.acc;
-      pv[vr] = out_state.seen;
-      ps[vr] = out_state.status;
-    }
+  } else {
+    out_state = exact_row_state<F, St, TPR, UNROLL, VECTOR>(rp, stride_col, c0, c1, t, n,
+                                                             lds_state);
+  }
+  if (live && t == 0) {
+    pm[vr] = out_state.m;
+    pa[vr] = out_state.acc;
+    pv[vr] = out_state.seen;
+    ps[vr] = out_state.status;
   }
 }
 

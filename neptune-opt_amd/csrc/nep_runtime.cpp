@@ -124,6 +124,10 @@ int compile_to_code(const char* source, const char* name, const char* options,
 // In-process module cache: exact (device, options, source) identity -> loaded module.  Kept
 // for the life of the process, like the reference's generated-module dictionaries.
 std::mutex g_mutex;
+// Split partial kernels looked up through nep_get_kernel -> the (row, part) pairs one of their
+// workgroups covers (the size of the unit's "<kernel>_parts_per_workgroup" marker symbol).
+std::map<uint64_t, uint32_t> g_split_parts;
+std::mutex g_split_mutex;
 std::map<std::tuple<int, std::string, std::string>, hipModule_t> g_modules;
 
 }  // namespace
@@ -211,6 +215,18 @@ int nep_get_kernel(uint64_t module, const char* kernel_name, uint64_t* kernel_ou
   if (err != hipSuccess)
     return hip_fail(err, (std::string("hipModuleGetFunction(") + kernel_name + ")").c_str());
   *kernel_out = reinterpret_cast<uint64_t>(fn);
+  // A split partial kernel's unit also holds its launch shape as a marker symbol's size.
+  const std::string marker = std::string(kernel_name) + "_parts_per_workgroup";
+  hipDeviceptr_t sym = nullptr;
+  size_t bytes = 0;
+  if (hipModuleGetGlobal(&sym, &bytes, reinterpret_cast<hipModule_t>(module), marker.c_str()) ==
+          hipSuccess &&
+      bytes > 0) {
+    std::lock_guard<std::mutex> lock(g_split_mutex);
+    g_split_parts[*kernel_out] = static_cast<uint32_t>(bytes);
+  } else {
+    (void)hipGetLastError();   // most kernels have no marker: leave no error behind
+  }
   return NEP_OK;
 }
 
@@ -318,18 +334,18 @@ int check_split(const char* who, uint64_t partial_kernel, uint64_t merge_kernel,
   if (nparts > kMaxSplitParts) return bad("nparts exceeds the split capacity of 4096 partials");
   if (partial_threads == 0 || partial_threads > 1024 || partial_threads % 64 != 0)
     return bad("partial_threads must be a multiple of 64 in [64, 1024]");
-  // Any value only sizes the grid: the partial kernel strides over the virtual rows.
   if (parts_per_workgroup == 0 || parts_per_workgroup > partial_threads)
     return bad("parts_per_workgroup must be in [1, partial_threads]");
   if (rows > (int64_t(1) << 40) / nparts) return bad("rows * nparts is too large");
   return NEP_OK;
 }
 
-// The partial kernel's lane mapping is compiled for its launch bound, and the merge kernel
-// runs 256-lane workgroups: both bounds are read from the kernels themselves (after the
-// argument checks, and only when there is work to launch).
+// The partial kernel's lane mapping is compiled for its launch bound and its (row, part)
+// pairs per workgroup, and the merge kernel runs 256-lane workgroups: the caller's numbers are
+// checked against what the kernels themselves hold (after the argument checks, and only when
+// there is work to launch).  A mismatch would leave partials unwritten.
 int check_split_kernels(const char* who, uint64_t partial_kernel, uint64_t merge_kernel,
-                        uint32_t partial_threads) {
+                        uint32_t partial_threads, uint32_t parts_per_workgroup) {
   int bound = 0;
   hipError_t err = hipFuncGetAttribute(&bound, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
                                        reinterpret_cast<hipFunction_t>(partial_kernel));
@@ -339,6 +355,20 @@ int check_split_kernels(const char* who, uint64_t partial_kernel, uint64_t merge
                                      std::to_string(partial_threads) +
                                      " differs from the partial kernel's workgroup size " +
                                      std::to_string(bound));
+  uint32_t parts = 0;
+  {
+    std::lock_guard<std::mutex> lock(g_split_mutex);
+    auto it = g_split_parts.find(partial_kernel);
+    if (it != g_split_parts.end()) parts = it->second;
+  }
+  if (parts == 0)
+    return fail(NEP_ERR_INVALID, std::string(who) +
+                                     ": partial_kernel is not a split partial kernel looked up "
+                                     "through nep_get_kernel");
+  if (parts_per_workgroup != parts)
+    return fail(NEP_ERR_INVALID, std::string(who) + ": parts_per_workgroup " +
+                                     std::to_string(parts_per_workgroup) +
+                                     " differs from the partial kernel's " + std::to_string(parts));
   err = hipFuncGetAttribute(&bound, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
                             reinterpret_cast<hipFunction_t>(merge_kernel));
   if (err != hipSuccess) return hip_fail(err, "hipFuncGetAttribute(split merge)");
@@ -353,7 +383,8 @@ int run_split(const char* who, uint64_t partial_kernel, uint64_t merge_kernel, c
               int64_t nparts, int64_t block, uint32_t partial_threads,
               uint32_t parts_per_workgroup, void* scratch_base, void* stream) {
   if (rows == 0) return NEP_OK;
-  int krc = check_split_kernels(who, partial_kernel, merge_kernel, partial_threads);
+  int krc = check_split_kernels(who, partial_kernel, merge_kernel, partial_threads,
+                                parts_per_workgroup);
   if (krc != NEP_OK) return krc;
   const int64_t count = rows * nparts;
   char* base = static_cast<char*>(scratch_base);

@@ -244,7 +244,13 @@ def _fold_kernel(sk: Skeleton, plan: str, part: str, var: FoldVariant) -> tuple[
                "long long rows, long long ncols, long long nparts")
         body = f"nep::fold_split_merge<Fold, {st}>(pm, pa, pv, ps, ({st}::T*)out, rows, ncols, nparts);"
     wg = 256 if part == "merge" else var.wg
-    return name, (f'extern "C" __global__ void __launch_bounds__({wg}) {name}({sig}) {{\n'
+    marker = ""
+    if part == "partial":
+        # the (row, part) pairs one workgroup covers, as the size of a marker symbol: the C ABI
+        # reads it with hipModuleGetGlobal (no copy) and checks the caller's launch numbers
+        marker = (f'extern "C" __device__ __attribute__((used)) unsigned char '
+                  f"{name}_parts_per_workgroup[{max(1, wg // var.tpr)}] = {{1}};\n")
+    return name, (marker + f'extern "C" __global__ void __launch_bounds__({wg}) {name}({sig}) {{\n'
                   f"  {body}\n}}\n")
 
 

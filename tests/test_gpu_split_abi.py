@@ -85,23 +85,25 @@ def test_split_entry_point_strided_rows_and_another_skeleton():
     assert torch.equal(got.view(torch.int32), want.view(torch.int32))
 
 
-def test_split_entry_point_checks_threads_and_any_grid_is_exact():
-    """partial_threads is checked against the partial kernel's own workgroup size (read from
-    the kernel, NEP_ERR_INVALID on a mismatch, nothing launched); parts_per_workgroup only sizes
-    the grid, since the partial kernel strides over the (row, part) pairs: fewer or more
-    workgroups than one pass give bit-identical results."""
+def test_split_entry_point_checks_the_launch_numbers_against_the_kernel():
+    """partial_threads and parts_per_workgroup are checked against what the generated unit
+    holds (the partial kernel's workgroup bound, and the size of its parts-per-workgroup marker
+    symbol): any other value fails with NEP_ERR_INVALID before any launch, while the kernel's
+    own numbers give the Python split path's result."""
     dev = _dev()
     g = torch.Generator().manual_seed(23)
     x = (4 * torch.randn(48, 20000, generator=g)).bfloat16().to(dev)
     want = CG.run("logsumexp", x, plan="split", block=1024)
     _, _, _, _, _, wg, rpw = split_call(x, "logsumexp", 1024)
     lib = hip.load_library()
-    for threads in {64, 128, 256, 512, 1024} - {wg}:
+    for threads in sorted({64, 128, 256, 512, 1024} - {wg}):
         print(f"nep_fold_split refuses partial_threads={threads} (kernel: {wg})", flush=True)
         run_entry(x, 1024, threads=threads, expect_rc=1)
-        assert "workgroup size" in lib.nep_last_error().decode()
-    for ppw in sorted({1, max(1, rpw // 2), rpw, min(wg, 2 * rpw), min(wg, 8 * rpw)}):
-        print(f"nep_fold_split parts_per_workgroup={ppw} (kernel: {rpw})", flush=True)
-        got = run_entry(x, 1024, ppw=ppw)
-        torch.cuda.synchronize()
-        assert torch.equal(_bits(got), _bits(want)), ppw
+        assert b"workgroup size" in lib.nep_last_error()
+    for ppw in sorted({1, max(1, rpw // 2), min(wg, 2 * rpw), min(wg, 8 * rpw)} - {rpw}):
+        print(f"nep_fold_split refuses parts_per_workgroup={ppw} (kernel: {rpw})", flush=True)
+        run_entry(x, 1024, ppw=ppw, expect_rc=1)
+        assert b"parts_per_workgroup" in lib.nep_last_error()
+    got = run_entry(x, 1024)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got), _bits(want))
