@@ -1,6 +1,6 @@
 """Benchmark of the fused dependent-reduction folds on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-folds] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-folds] [--no-cpu] [--no-pmc]
 
 Headline workload: the bf16 logsumexp / softmax-denominator fold
 over 16384 rows at widths {128, 1000, 4096, 32000} plus the split plan on 64 x 262144.
@@ -9,7 +9,11 @@ graph.  `value` = algorithmic bytes of a step / step time (GB/s).  `roofline` is
 kernel (width 32000) timed with HIP events around a graph of back-to-back launches on its
 stream, its input larger than the 256 MB Infinity Cache (cold).  `per_fold` reports every
 configuration of BASELINE.json the same way (inputs rotated over > 512 MB so each launch is
-cold).  `cpu_baseline` times the oracle's eager CPU restatement on a bounded row sample.
+cold).  `roofline.traffic` is the dominant kernel's HBM bytes per launch from two rocprofv3
+--pmc passes (FETCH_SIZE, WRITE_SIZE) run in child processes during this run, each counter
+scaled by its reading of a 256 MiB copy (the committed summary when rocprofv3 is unavailable
+or --no-pmc is given; `traffic_source` says which).  `cpu_baseline` times the oracle's eager
+CPU restatement on a bounded row sample.
 """
 from __future__ import annotations
 
@@ -350,17 +354,75 @@ def cpu_baseline(xs_cpu, seconds_target: float = 15.0):
                       "rounded to bf16"}
 
 
-def pmc_traffic():
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's reading of a plain copy of
-    known size), or None when the summary is absent."""
-    path = ROOT / "profiles" / "logsumexp_bf16_16384x32000_pmc.md"
-    if not path.exists():
+DOMINANT_KERNEL = "logsumexp_serial_bf16"      # prefix of the dominant kernel's name
+COPY_KERNEL = "copyBuffer"                     # torch's 256 MiB device copy in --pmc-probe
+COPY_KIB = 256 * 1024
+
+
+def _pmc_pass(counter: str, timeout_s: int = 120) -> dict | None:
+    """One rocprofv3 --pmc pass of `counter` over `bench.py --pmc-probe` in a child process:
+    mean KiB per dispatch of the dominant kernel and of the 256 MiB copy, or None."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    tool = shutil.which("rocprofv3")
+    if tool is None:
         return None
-    for line in path.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":", 1)[1].strip())
-    return None
+    out_dir = tempfile.mkdtemp(prefix="nep_pmc_", dir="/tmp")
+    env = dict(os.environ, TMPDIR="/tmp")
+    cmd = ["timeout", "-s", "KILL", str(timeout_s), tool, "--pmc", counter, "-f", "csv",
+           "-d", out_dir, "-o", counter.lower(), "--", sys.executable, str(ROOT / "bench.py"),
+           "--pmc-probe"]
+    try:
+        subprocess.run(cmd, env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                       timeout=timeout_s + 30, check=False)
+        files = sorted(pathlib.Path(out_dir).rglob("*counter_collection.csv"))
+        if not files:
+            return None
+        sums: dict = {"dominant": [], "copy": []}
+        with open(files[0], newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name, value = row.get("Kernel_Name", ""), float(row.get("Counter_Value", "nan"))
+                if name.startswith(DOMINANT_KERNEL):
+                    sums["dominant"].append(value)
+                elif COPY_KERNEL in name:
+                    sums["copy"].append(value)
+        if not sums["dominant"] or not sums["copy"]:
+            return None
+        return {k: sum(v) / len(v) for k, v in sums.items()}
+    except (OSError, ValueError, subprocess.SubprocessError):
+        return None
+    finally:
+        shutil.rmtree(out_dir, ignore_errors=True)
+
+
+def pmc_traffic(live: bool = True) -> tuple:
+    """(HBM bytes per launch of the dominant kernel, how it was obtained).  Live: two rocprofv3
+    --pmc passes in child processes (FETCH_SIZE, then WRITE_SIZE), each counter scaled by its
+    own reading of a 256 MiB device copy of known size.  Otherwise, or when a pass fails, the
+    committed summary profiles/logsumexp_bf16_16384x32000_pmc.md."""
+    if live and not any(k.startswith("ROCPROF") for k in os.environ) \
+            and "rocprof" not in os.environ.get("LD_PRELOAD", ""):
+        fetch, write = _pmc_pass("FETCH_SIZE"), None
+        if fetch is not None:
+            write = _pmc_pass("WRITE_SIZE")
+        if fetch is not None and write is not None:
+            fs, ws = COPY_KIB / fetch["copy"], COPY_KIB / write["copy"]
+            traffic = int(round((fetch["dominant"] * fs + write["dominant"] * ws) * 1024))
+            return traffic, {"source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE in this run",
+                             "fetch_KiB": round(fetch["dominant"], 1),
+                             "write_KiB": round(write["dominant"], 1),
+                             "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
+    path = ROOT / "profiles" / "logsumexp_bf16_16384x32000_pmc.md"
+    if path.exists():
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip()), {"source": str(path.relative_to(ROOT))}
+    return None, {"source": "unavailable"}
 
 
 READ_PROBE_SRC = r'''
@@ -533,6 +595,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-folds", action="store_true", help="skip the per-configuration table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-pmc", action="store_true",
+                    help="take roofline.traffic from the committed PMC summary instead of two "
+                         "rocprofv3 --pmc passes in child processes")
     ap.add_argument("--pmc-probe", nargs="?", const="dominant", default=None,
                     choices=("dominant", "all"),
                     help="only run the dominant kernel (or, with 'all', also RMSNorm, segment "
@@ -637,8 +702,10 @@ def main():
     dom_ms = graph_time(lambda i: CG.run("logsumexp", x32), replays=5, inner=20)
     dom_bytes = cfg2_bytes(32000)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    traffic, traffic_source = pmc_traffic(live=not args.no_pmc)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK, 4), "traffic": pmc_traffic(),
+                "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic,
+                "traffic_source": traffic_source,
                 "kernel": "logsumexp_serial_bf16 (16384 x 32000)", "kernel_us": round(dom_ms * 1e3, 2),
                 "bytes_per_launch": dom_bytes}
     log(f"[bench] dominant kernel {dom_ms * 1e3:.1f} us, {achieved:.1f} GB/s")
