@@ -9,9 +9,10 @@ package (test infrastructure), not here.
 """
 from __future__ import annotations
 
-from neptune_codegen import library  # noqa: F401  (populates SKELETONS)
-from neptune_codegen.algebra import (MergeCertificate, StateCertificate, _as_quotient_power,
-                                     _marked, _simplify, coordinate_needs_floor,
+from neptune_codegen import hip, library  # noqa: F401  (library populates SKELETONS)
+from neptune_codegen.algebra import (_BRANCH_CUT, MergeCertificate, StateCertificate, _Q,
+                                     _as_quotient_power, _marked, _numerically_zero, _simplify,
+                                     coordinate_needs_floor,
                                      derive_merge_certificate, derive_state_certificate,
                                      reachable_producer_domain, repair_bias, repair_factor,
                                      repair_pair, term_expr, vanishes)
@@ -27,12 +28,12 @@ from neptune_codegen.skeleton import (NEGATIVE_CONTROLS, SKELETONS, STATE_REDUCT
                                       state_reduction_spec, supported, unsupported_reason)
 from neptune_codegen.sym_to_hip import TranslationError, to_hip
 from neptune_codegen.symbols import *  # noqa: F401,F403
-from neptune_codegen.template import (MAX_SPLIT_PARTS, compile_skeleton, compile_state_reduction,
+from neptune_codegen.template import (_CACHE, MAX_SPLIT_PARTS, compile_skeleton, compile_state_reduction,
                                       compile_readout, generated_path, launch_reduction,
                                       launch_rms_norm, run, run_l2_normalize, run_log_softmax,
                                       run_readout, run_rms_norm, split_launch_shape,
                                       validate_l2_inputs, validate_plan, validate_rms_inputs)
-from neptune_codegen.torch_op import (as_hip_op, as_readout_op, as_segment_op, as_state_op,
+from neptune_codegen.torch_op import (_TRITON_OPS, as_hip_op, as_readout_op, as_segment_op, as_state_op,
                                       as_triton_op, compile_segment_reduction, op_handle,
                                       readout_op_handle, run_segment_pool,
                                       segment_op_handle, state_op_handle, triton_op_name,
@@ -66,4 +67,10 @@ __all__ = [
     "run_attention", "attention_fold", "as_attention_op", "launch_attention", "exact_path_taken",
     "compile_readout", "run_readout", "run_log_softmax", "as_readout_op", "readout_op_handle",
     "best_config", "machine_key", "op_key", "parameter_tag", "prebuilt_programs",
+    # internals the reference package also exports: the algebra's quotient-power marker and
+    # numeric zero filter with its branch-cut list, the compiled-unit cache, the op registry
+    # (HIP ops, under the reference's name) and the directory of generated artefacts (here
+    # the code-object cache)
+    "_Q", "_numerically_zero", "_BRANCH_CUT", "_CACHE", "_TRITON_OPS", "_GEN_DIR",
 ]
+_GEN_DIR = str(hip.CACHE_DIR)

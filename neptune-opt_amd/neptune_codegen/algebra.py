@@ -29,6 +29,7 @@ from neptune_codegen.symbols import *  # noqa: F401,F403
 
 # Residuals containing these may vanish on sympy's principal branch only.
 _BRANCH_FUNCS = (sp.log, sp.atanh, sp.acosh, sp.atan, sp.acos, sp.asin)
+_BRANCH_CUT = _BRANCH_FUNCS   # the reference package's name for the same tuple
 
 
 class _Q(sp.Function):

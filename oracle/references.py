@@ -72,6 +72,40 @@ def reference(name: str, x, **params):
     raise KeyError(name)
 
 
+def graph_reference(name: str, x, **params):
+    """The same skeleton in decomposed form (references.py:100-140): the producer reduction is
+    a separate tensor, then the consumer's terms are summed (or maxed) against it and read out
+    -- the graph Inductor would otherwise compile, with its materialised intermediate."""
+    import torch
+
+    p = {**_defaults(name), **params}
+    t = x.reshape(x.shape[0], -1).float()
+    n = t.shape[-1]
+    lse_operand = {"logsumexp": lambda v: v, "lse_biased": lambda v: v + p["alpha"],
+                   "softcap_lse": lambda v: torch.tanh(p["beta"] * v),
+                   "lse_scaled": lambda v: v / p["T"]}
+    if name in lse_operand:
+        z = lse_operand[name](t)
+        m = z.amax(dim=-1, keepdim=True)                       # producer: row max
+        acc = torch.exp(z - m).sum(dim=-1, keepdim=True)       # consumer: sum of exp(phi - m)
+        return (m + torch.log(acc)).squeeze(-1)
+    if name == "rmsnorm_max":
+        r = (t * t).sum(dim=-1, keepdim=True) / n              # producer: mean of squares
+        return (t / torch.sqrt(r + p["eps"])).amax(dim=-1)    # consumer: max of the terms
+    if name in ("variance", "std"):
+        mu = t.sum(dim=-1, keepdim=True) / n                   # producer: mean (first pass)
+        var = ((t - mu) ** 2).sum(dim=-1) / n                  # consumer: centred second pass
+        return var if name == "variance" else torch.sqrt(var)
+    m = t.abs().amax(dim=-1, keepdim=True).clamp_min(1e-30)  # producer: floored max |x|
+    terms = {"stable_l2": lambda: (t / m) ** 2, "sumsq_div": lambda: (t * t) / m,
+             "linear_attn": lambda: t / m, "decay_renorm": lambda: t / (m + p["N"])}
+    if name not in terms:
+        raise KeyError(name)
+    acc = terms[name]().sum(dim=-1, keepdim=True)
+    out = m * torch.sqrt(acc) if name == "stable_l2" else acc
+    return out.squeeze(-1)
+
+
 def rms_norm_reference(x, gamma, eps=1e-6):
     """fp32 promote -> square/mean/eps/rsqrt/normalize -> round to dtype -> * gamma."""
     source = x.float()

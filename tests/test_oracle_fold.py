@@ -126,3 +126,24 @@ def test_attention_fold_matches_closed_form(causal):
     np.testing.assert_allclose(lse, torch.logsumexp(s, -1).numpy(), rtol=1e-12, atol=1e-12)
     ref = R.attention_reference(q.float(), k.float(), v.float(), scale=0.25, causal=causal)
     np.testing.assert_allclose(ref.double().numpy(), o, rtol=1e-4, atol=1e-5)
+
+
+def _skeleton_names():
+    from neptune_codegen.skeleton import SKELETONS
+
+    return sorted(SKELETONS)
+
+
+@pytest.mark.parametrize("name", _skeleton_names())
+def test_graph_reference_matches_the_fused_closed_form(name):
+    """graph_reference (the decomposed producer-then-consumer form) equals reference (torch's
+    fused closed forms: logsumexp, var/std, ...) on rows with mixed signs and a zero row; a
+    slip in either decomposition -- a dropped max shift, a wrong divisor, the floor on the
+    wrong side -- would show here."""
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(9, 300, generator=g) * torch.tensor([0.01, 1.0, 30.0]).repeat(3)[:, None]
+    x[4] = 0.0
+    x[5, :7] = 80.0
+    want = R.reference(name, x)
+    got = R.graph_reference(name, x)
+    torch.testing.assert_close(got, want, rtol=2e-5, atol=1e-6, equal_nan=True)
