@@ -283,3 +283,36 @@ def test_attention_custom_op():
     got = op(q.to(dev), k.to(dev), v.to(dev))
     torch.testing.assert_close(got.cpu().float(), R.attention_reference(q, k, v).float(),
                                rtol=1.6e-2, atol=1e-3)
+
+
+def test_attention_graph_replays_match_eager_and_launch_two_kernels():
+    """run_attention is the V^T pack and the fold, nothing else (no fill, no assert, no
+    synchronisation), so it captures into a HIP graph.  Replays with other eager work between
+    them give the eager result every time, also for a block that takes the exact path."""
+    from neptune_codegen import hip as H
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(19)
+    q, k, v = (torch.randn(1, 3, 300, 128, generator=g).bfloat16().to(dev) for _ in range(3))
+    v[0, 2, 260, 1] = float("inf")            # head 2, query block 1: exact path
+    with H.recording() as rec:
+        want, want_lse = CG.run_attention(q, k, v, causal=True, return_lse=True)
+    assert len(rec.launches) == 2
+    torch.cuda.synchronize()
+    _say("attention graph capture, 3 replays")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            out, lse = CG.run_attention(q, k, v, causal=True, return_lse=True)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(3):
+        out.zero_()
+        lse.zero_()
+        graph.replay()
+        torch.randn(1000, device=dev).sum()   # unrelated eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(torch.isnan(out), torch.isnan(want)), i
+        assert torch.equal(out.nan_to_num(0.0, 1.0, -1.0), want.nan_to_num(0.0, 1.0, -1.0)), i
+        assert torch.equal(lse, want_lse), i
