@@ -383,14 +383,16 @@ def _pmc_pass(counter: str, timeout_s: int = 120) -> dict | None:
             return None
         sums: dict = {"dominant": [], "copy": []}
         with open(files[0], newline="") as fh:
-            for row in csv.DictReader(fh):
-                if row.get("Counter_Name") != counter:
-                    continue
-                name, value = row.get("Kernel_Name", ""), float(row.get("Counter_Value", "nan"))
-                if name.startswith(DOMINANT_KERNEL):
-                    sums["dominant"].append(value)
-                elif COPY_KERNEL in name:
-                    sums["copy"].append(value)
+            found = sorted((r for r in csv.DictReader(fh) if r.get("Counter_Name") == counter),
+                           key=lambda r: int(r.get("Dispatch_Id", 0)))
+        for row in found:
+            name, value = row.get("Kernel_Name", ""), float(row.get("Counter_Value", "nan"))
+            if name.startswith(DOMINANT_KERNEL):
+                sums["dominant"].append(value)
+            elif COPY_KERNEL in name and sums["dominant"]:
+                # only the probe's 256 MiB copies, which follow the first dominant launch
+                # (input uploads before it may run small copy kernels of their own)
+                sums["copy"].append(value)
         if not sums["dominant"] or not sums["copy"]:
             return None
         return {k: sum(v) / len(v) for k, v in sums.items()}
