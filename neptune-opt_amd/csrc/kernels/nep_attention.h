@@ -51,8 +51,10 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kAttnWaves = 8;          // wave64s per fold workgroup (32 queries each)
-constexpr int kAttnBM = 32 * kAttnWaves;   // queries per fold workgroup
+// wave64s per fold workgroup (32 queries each): two per SIMD up to head dim 128; at head dim
+// 256 a wave's O^T and Q^T operands alone take 192 registers, so one wave per SIMD
+template <int D>
+constexpr int attn_waves() { return D <= 128 ? 8 : 4; }
 constexpr int kAttnBN = 64;            // keys per tile
 constexpr int kAttnThreads = 256;      // V^T pack workgroup: 4 wave64s
 constexpr float kRescaleSlack = 8.0f;  // base-2 headroom before the reference max moves
@@ -109,12 +111,12 @@ __device__ __forceinline__ int vt_slot(int key) {
 
 // LDS rows are read 16 bytes per lane, 16 consecutive rows per LDS cycle (64 banks of 4 bytes,
 // 256 bytes per clock).  Row r keeps its 16-byte chunk c at position c ^ swizzle<CH>(r), so the
-// 16 rows of one cycle hit 16 different bank groups: rows of 16+ chunks XOR with r % 16, rows of
-// 8 chunks (128 bytes: two rows per 256-byte bank sweep) XOR with (r / 2) % 8.
+// 16 rows of one cycle hit 16 different bank groups: rows of 16 or 32 chunks XOR with r % 16,
+// rows of 8 chunks (128 bytes: two rows per 256-byte bank sweep) XOR with (r / 2) % 8.
 template <int CH>
 __device__ __forceinline__ int swizzle(int row) {
-  static_assert(CH == 8 || CH == 16, "rows of 8 or 16 chunks");
-  if constexpr (CH == 16) return row & 15;
+  static_assert(CH == 8 || CH == 16 || CH == 32, "rows of 8, 16 or 32 chunks");
+  if constexpr (CH >= 16) return row & 15;
   else return (row >> 1) & 7;
 }
 
@@ -130,7 +132,7 @@ __device__ __forceinline__ void attention_vt_pack(const T* __restrict__ v, u16* 
   constexpr int CH = D / 8;                         // 16-byte chunks per key row
   constexpr int UNITS = (kAttnBN / 2) * CH;         // (key pair, dim chunk) units
   constexpr int UPT = UNITS / kAttnThreads;
-  static_assert(UNITS % kAttnThreads == 0, "head dim must be 64 or 128");
+  static_assert(UNITS % kAttnThreads == 0, "head dim must be 64, 128 or 256");
   __shared__ __attribute__((aligned(16))) u16 img[D * kAttnBN];
   __shared__ u32 wave_max[kAttnThreads / 64];
   __shared__ int wave_bad[kAttnThreads / 64];
@@ -304,16 +306,16 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* dst, in
 // score is the group sum of their partial dot products, and (m, l, O) are moved to every new
 // maximum exactly (not lazily).  Masked keys contribute nothing, so only the rows that see a
 // non-finite V value turn non-finite, as IEEE arithmetic on the visible keys gives.
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, int W>
 __device__ void attention_exact_rows(const T* __restrict__ qp, const T* __restrict__ kp,
                                      const T* __restrict__ vp, T* __restrict__ orow0,
                                      float* __restrict__ lse_row0, int sq, int sk, int q0,
                                      i64 qss, i64 kss, i64 vss, float scale_log2) {
   typedef AttnIn<T> In;
   constexpr int DQ = D / 4;                    // head dims per lane
-  constexpr int ROWS = kAttnWaves * 64 / 4;    // queries per round
+  constexpr int ROWS = W * 64 / 4;             // queries per round
   const int tid = threadIdx.x, c = tid & 3;
-  for (int r0 = q0; r0 < q0 + kAttnBM; r0 += ROWS) {
+  for (int r0 = q0; r0 < q0 + 32 * W; r0 += ROWS) {
     const int my_q = r0 + (tid >> 2);
     const bool active = my_q < sq;
     float qv[DQ], ov[DQ];
@@ -394,16 +396,18 @@ __device__ __forceinline__ void attention_fwd(const T* __restrict__ q, const T* 
                                               i64 qsb, i64 qsh, i64 qss, i64 ksb, i64 ksh,
                                               i64 kss, i64 vsb, i64 vsh, i64 vss, int e_max,
                                               float scale_log2) {
-  static_assert(D == 64 || D == 128, "head dim must be 64 or 128");
+  static_assert(D == 64 || D == 128 || D == 256, "head dim must be 64, 128 or 256");
   typedef AttnIn<T> In;
   typedef typename In::vec8 vec8;
+  constexpr int kAttnWaves = attn_waves<D>();
+  constexpr int kAttnBM = 32 * kAttnWaves;           // queries per workgroup
   constexpr int CH = D / 8;                          // 16-byte chunks per K row
   constexpr int KSTEPS = D / 16;                     // MFMA k-steps of S^T
   constexpr int DBLK = D / 32;                       // 32-row blocks of O^T
   constexpr int TILE = kAttnBN * D * 2;              // bytes of one K tile (= one V^T tile)
   constexpr int PIECES = TILE / 1024 / kAttnWaves;   // 1 KB DMA blocks per wave and operand
   constexpr int KROWS = 1024 * kAttnWaves / (CH * 16);   // K rows per DMA round of all waves
-  static_assert(PIECES >= 1 && KROWS % 16 == 0, "DMA mapping");
+  static_assert(PIECES >= 1 && KROWS >= 1, "DMA mapping");
   // Separate arrays per buffer: the compiler then proves that LDS reads of one buffer do not
   // depend on DMA into the other and does not wait for it.
   __shared__ __attribute__((aligned(1024))) unsigned char kbuf0[TILE];
@@ -443,11 +447,14 @@ __device__ __forceinline__ void attention_fwd(const T* __restrict__ q, const T* 
 
   // DMA addressing.  LDS chunk L = (i*W + wave)*64 + lane (W waves) of a K tile is key L / CH, position
   // L % CH, and holds head-dim chunk (L % CH) ^ swizzle<CH>(key) of that key; piece i moves
-  // KROWS keys further (KROWS is a multiple of 16, so the swizzle does not depend on i).
-  int koff0;
-  {
-    const int chunk = wave * 64 + lane, key = chunk / CH, p = chunk % CH;
-    koff0 = (int)((i64)key * kss * 2) + ((p ^ swizzle<CH>(key)) << 4);
+  // KROWS keys further.  When KROWS is a multiple of 16 the swizzle does not depend on i and one
+  // offset serves every piece; otherwise (head dim 256: 8 keys per round) each piece has its own.
+  constexpr int KOFFS = KROWS % 16 == 0 ? 1 : PIECES;
+  int koffs[KOFFS];
+#pragma unroll
+  for (int i = 0; i < KOFFS; ++i) {
+    const int chunk = (i * kAttnWaves + wave) * 64 + lane, key = chunk / CH, p = chunk % CH;
+    koffs[i] = (int)((i64)key * kss * 2) + ((p ^ swizzle<CH>(key)) << 4);
   }
   const int kstep = (int)((i64)KROWS * kss * 2);
   // K(tile) and V^T(tile) into LDS; keys at or past sk read as zero (buffer range check),
@@ -462,7 +469,8 @@ __device__ __forceinline__ void attention_fwd(const T* __restrict__ q, const T* 
         (void*)(vth + (i64)tile * (D * kAttnBN)), (short)0, TILE, (int)kRawBufferWord3);
 #pragma unroll
     for (int i = 0; i < PIECES; ++i) {
-      dma16(rk, kdst + (i * kAttnWaves + wave) * 1024, koff0 + i * kstep, 0);
+      if constexpr (KOFFS == 1) dma16(rk, kdst + (i * kAttnWaves + wave) * 1024, koffs[0] + i * kstep, 0);
+      else dma16(rk, kdst + (i * kAttnWaves + wave) * 1024, koffs[i], 0);
       dma16(rv, vdst + (i * kAttnWaves + wave) * 1024, lane * 16, (i * kAttnWaves + wave) * 1024);
     }
   };
@@ -595,8 +603,9 @@ __device__ __forceinline__ void attention_fwd(const T* __restrict__ q, const T* 
   T* orow0 = o + (i64)bh * sq * D;
   float* lse_row0 = lse != nullptr ? lse + (i64)bh * sq : nullptr;
   if (exact) {
-    attention_exact_rows<T, D, CAUSAL>(qp, kp, v + b * vsb + h * vsh, orow0, lse_row0, sq, sk,
-                                       q0, qss, kss, vss, scale_log2);
+    attention_exact_rows<T, D, CAUSAL, kAttnWaves>(qp, kp, v + b * vsb + h * vsh, orow0,
+                                                   lse_row0, sq, sk, q0, qss, kss, vss,
+                                                   scale_log2);
     return;
   }
   // ---- readout: O / l, and the natural-log LSE of the scaled scores

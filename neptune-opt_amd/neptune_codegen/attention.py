@@ -6,8 +6,8 @@ exp(s - s2) (tests/test_neptune_opt.py:347) applied per key tile to the running
 (max, sum, output) state, with MFMA for Q K^T and P V.  The causal mask is torch's
 `is_causal=True` (query i sees keys j <= i).  The oracle is the closed form in fp32.
 
-Layout contract: q [B, H, Sq, D], k/v [B, H, Sk, D], one dtype (bf16 or fp16), unit stride
-on D; other strides are honoured (rows must be 16-byte aligned, otherwise the input is made
+Layout contract: q [B, H, Sq, D], k/v [B, H, Sk, D], D in {64, 128, 256}, one dtype (bf16 or
+fp16), unit stride on D; other strides are honoured (rows must be 16-byte aligned, otherwise the input is made
 contiguous).  Output is a fresh contiguous [B, H, Sq, D] tensor of the input dtype;
 `return_lse` adds the fp32 [B, H, Sq] natural-log logsumexp of the scaled, masked scores.
 
@@ -24,14 +24,15 @@ import math
 import threading
 
 from neptune_codegen import hip
-from neptune_codegen.emitters import (ATTN_FOLD_THREADS, BASE_OPTIONS, attention_kernel_name,
+from neptune_codegen.emitters import (ATTN_HEAD_DIMS, BASE_OPTIONS, attention_block_m,
+                                      attention_fold_threads, attention_kernel_name,
                                       attention_pack_kernel_name, emit_attention_source)
 
 _PROGRAMS: dict = {}
 _OPS: dict = {}
 _lock = threading.Lock()
 LOG2E = 1.4426950408889634
-BLOCK_M = 256           # queries per fold workgroup (8 waves of 32)
+BLOCK_M = 256           # queries per fold workgroup up to head dim 128 (8 waves of 32)
 BLOCK_N = 64            # keys per tile (one V^T image per tile)
 K_ROW_STRIDE_MAX = 1 << 24   # K rows are addressed with 32-bit byte offsets within a tile
 # V^T tiles are fp16 images of v * 2^-e, e the tile's exponent (0 below 2^15).  A tile value
@@ -71,8 +72,8 @@ def validate_attention_inputs(q, k, v, *, metadata: bool = False):
         raise TypeError(f"attention q, k, v must share one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
     if q.device != k.device or q.device != v.device:
         raise ValueError("attention tensors must be on the same device")
-    if q.shape[3] not in (64, 128):
-        raise NotImplementedError("attention fold supports head_dim 64 and 128")
+    if q.shape[3] not in ATTN_HEAD_DIMS:
+        raise NotImplementedError("attention fold supports head_dim 64, 128 and 256")
     if k.shape[2] == 0:
         raise ValueError("attention needs at least one key")
     return tuple(q.shape)
@@ -128,12 +129,12 @@ def _launch(q, k, v, scale, causal, return_lse, e_max: int):
                        (hip.PTR,) * 3 + (hip.I32,) * 2 + (hip.I64,) * 3, 256, device)
     fold = prog.kernel(attention_kernel_name(D, causal, q.dtype),
                        (hip.PTR,) * 7 + (hip.I32,) * 3 + (hip.I64,) * 9 + (hip.I32, hip.F32),
-                       ATTN_FOLD_THREADS, device)
+                       attention_fold_threads(D), device)
     stream = hip.current_stream(q.device)
     pack.launch((B * H * ntiles,),
                 (v.data_ptr(), vt.data_ptr(), exps.data_ptr(), H, Sk,
                  v.stride(0), v.stride(1), v.stride(2)), stream)
-    nqb = (Sq + BLOCK_M - 1) // BLOCK_M
+    nqb = (Sq + attention_block_m(D) - 1) // attention_block_m(D)
     fold.launch((nqb * B * H,),
                 (q.data_ptr(), k.data_ptr(), vt.data_ptr(), exps.data_ptr(), v.data_ptr(),
                  out.data_ptr(), lse.data_ptr() if lse is not None else 0, H, Sq, Sk,

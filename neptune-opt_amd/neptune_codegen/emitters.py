@@ -527,9 +527,23 @@ def segment_kernel_name(name: str, var: SegmentVariant) -> str:
 
 
 # ---------------------------------------------------------------- attention fold
-# Two waves per SIMD for the attention fold (one 8-wave workgroup per CU, <= 256 VGPRs).
-ATTN_WAVES_PER_EU = 2
-ATTN_FOLD_THREADS = 512
+# The attention fold's workgroup: 8 wave64s (two per SIMD, <= 256 VGPRs each) up to head dim
+# 128, 4 (one per SIMD) at head dim 256; one workgroup per CU either way.
+ATTN_HEAD_DIMS = (64, 128, 256)
+
+
+def attention_waves(head_dim: int) -> int:
+    return 8 if head_dim <= 128 else 4
+
+
+def attention_fold_threads(head_dim: int) -> int:
+    return 64 * attention_waves(head_dim)
+
+
+def attention_block_m(head_dim: int) -> int:
+    """Queries per fold workgroup (32 per wave)."""
+    return 32 * attention_waves(head_dim)
+
 
 
 ATTN_DTYPES = {"bfloat16": ("bf16", "__bf16"), "float16": ("f16", "_Float16")}
@@ -547,9 +561,10 @@ def emit_attention_source(head_dim: int, causal: bool, dtype="bfloat16",
     """hiprtc unit of the online-softmax attention fold (no reference counterpart): the
     logsumexp repair exp(s - s2) applied per key tile to (m, l, O).  Holds two kernels: the
     V^T tile packer and the fold itself (with its exact fallback for out-of-range V)."""
-    wpe = ATTN_WAVES_PER_EU if waves_per_eu is None else waves_per_eu
-    if head_dim not in (64, 128):
-        raise NotImplementedError("attention fold supports head_dim 64 and 128")
+    if head_dim not in ATTN_HEAD_DIMS:
+        raise NotImplementedError("attention fold supports head_dim 64, 128 and 256")
+    wpe = attention_waves(head_dim) // 4 if waves_per_eu is None else waves_per_eu
+    threads = attention_fold_threads(head_dim)
     tag, ctype = _attn_dtype(dtype)
     name = attention_kernel_name(head_dim, causal, dtype)
     pack = attention_pack_kernel_name(head_dim, dtype)
@@ -562,7 +577,7 @@ def emit_attention_source(head_dim: int, causal: bool, dtype="bfloat16",
         "int heads, int sk, long long vsb, long long vsh, long long vss) {\n"
         f"  nep::attention_vt_pack<{ctype}, {head_dim}>((const {ctype}*)v, (nep::u16*)vt, exps, "
         "heads, sk, vsb, vsh, vss);\n}\n",
-        f'extern "C" __global__ void __launch_bounds__({ATTN_FOLD_THREADS}, {wpe}) {name}(const void* q, const void* k, '
+        f'extern "C" __global__ void __launch_bounds__({threads}, {wpe}) {name}(const void* q, const void* k, '
         "const void* vt, const int* exps, const void* v, void* o, float* lse, int heads, int sq, "
         "int sk, long long qsb, long long qsh, long long qss, long long ksb, long long ksh, "
         "long long kss, long long vsb, long long vsh, long long vss, int e_max, float scale_log2) {\n"

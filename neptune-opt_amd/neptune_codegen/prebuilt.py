@@ -75,7 +75,8 @@ def _attention_programs():
     from neptune_codegen.attention import _program
 
     return [_program(128, True), _program(128, False), _program(64, True), _program(64, False),
-            _program(128, True, "float16"), _program(64, False, "float16")]
+            _program(128, True, "float16"), _program(64, False, "float16"), _program(256, True),
+            _program(256, False), _program(256, True, "float16")]
 
 
 def programs():

@@ -70,7 +70,8 @@ def _lse_reference(q, k, causal, scale=None):
 
 SHAPES = [(1, 2, 256, 256, 128), (2, 3, 200, 200, 128), (1, 1, 77, 77, 128),
           (1, 2, 130, 333, 64), (1, 1, 1, 64, 128), (1, 4, 512, 512, 64),
-          (1, 2, 333, 130, 128), (2, 1, 700, 65, 64)]
+          (1, 2, 333, 130, 128), (2, 1, 700, 65, 64), (1, 2, 300, 300, 256),
+          (1, 1, 130, 333, 256), (2, 1, 1, 70, 256)]
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -91,7 +92,7 @@ def test_attention_parity(shape, causal):
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("shape", [(1, 2, 256, 256, 128), (2, 3, 200, 200, 128), (1, 2, 130, 333, 64),
-                                   (1, 1, 1, 64, 128), (2, 1, 700, 65, 64)])
+                                   (1, 1, 1, 64, 128), (2, 1, 700, 65, 64), (1, 2, 200, 200, 256)])
 def test_attention_parity_fp16(shape, causal):
     """fp16 Q/K/V: the f16 MFMA for Q K^T, the same fp16 P.V, an fp16 output."""
     dev = _dev()
@@ -128,7 +129,8 @@ def test_attention_fp16_values_at_the_top_of_the_range():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("shape", [(1, 2, 256, 256, 128), (1, 1, 300, 333, 64), (2, 1, 77, 77, 128)])
+@pytest.mark.parametrize("shape", [(1, 2, 256, 256, 128), (1, 1, 300, 333, 64), (2, 1, 77, 77, 128),
+                                   (1, 1, 200, 150, 256)])
 def test_attention_exact_path_matches_the_fp32_closed_form(shape, causal, dtype):
     """The exact fp32 path (forced for every query block by an exponent threshold of -1): fp32
     scores, fp32 P, the caller's V.  Its O is within the storage rounding of the fp32 closed
