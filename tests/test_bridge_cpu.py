@@ -259,3 +259,9 @@ def test_attention_validation():
     with pytest.raises(ValueError, match="device"):
         x = torch.empty(1, 1, 4, 64, dtype=torch.bfloat16)
         CG.run_attention(x, x, x)
+    for d, dt in ((256, torch.bfloat16), (64, torch.float16), (256, torch.float16)):
+        x = meta((1, 2, 16, d), dt)
+        out = CG.run_attention(x, x, x)
+        assert out.shape == x.shape and out.dtype == dt
+    with pytest.raises(TypeError, match="one dtype"):
+        CG.run_attention(q, meta((1, 2, 16, 128), torch.float16), q)
