@@ -75,6 +75,19 @@ __device__ __forceinline__ float rms_readout(float v, float g, float scale) {
   }
 }
 
+// v / s rounded correctly, with the row's reciprocal y = RN(1/s) shared by its elements:
+// q0 = RN(v*y) is within one ulp of v/s, the remainder r = q0*s - v is exact in one FMA, and
+// RN(q0 - r*y) is the correctly rounded quotient (Markstein's correction).  Holds for s and
+// 1/s normal, v zero (either sign) or |v| >= 2^-100 (below that the remainder can underflow),
+// and a normal or zero quotient; the caller sends every other element through div_rn.  Checked
+// against IEEE division on the host (tests/csrc/div_by_row_check.c): 2.8e8 random pairs and
+// every fp32 v in [2^-100, 2), both signs, for eight divisors, without a difference.
+__device__ __forceinline__ float div_by_row(float v, float s, float y) {
+  const float q0 = v * y;
+  const float r = __builtin_fmaf(q0, s, -v);
+  return __builtin_fmaf(-r, y, q0);
+}
+
 template <bool L2>
 __device__ __forceinline__ float rms_scale(float total, float count, float eps) {
   if constexpr (L2) {
@@ -102,18 +115,15 @@ __device__ __forceinline__ void rms_serial(const typename St::T* __restrict__ x,
   const int t = threadIdx.x % TPR;
   const float count = (float)ncols;
   if constexpr (VECTOR) {
-    // gamma is staged once per workgroup in LDS and re-read per row: held in registers it
-    // would stay unpacked across the row loop (64 VGPRs per lane) and halve the occupancy.
-    __shared__ u32x4 gsh[L2 ? 1 : NV * TPR];
+    // gamma stays in registers as packed words (NV per lane) and is unpacked at its use: no LDS
+    // staging and no barrier before the first row (84.1 -> 83.7 us at cfg3).
+    u32x4 gr[L2 ? 1 : NV];
     if constexpr (!L2) {
-      if (threadIdx.x < TPR) {
 #pragma unroll
-        for (int u = 0; u < NV; ++u) {
-          const i64 e = (i64)(u * TPR + t) * VEC;
-          gsh[u * TPR + t] = e < ncols ? load16_cached(gamma + e) : u32x4{0u, 0u, 0u, 0u};
-        }
+      for (int u = 0; u < NV; ++u) {
+        const i64 e = (i64)(u * TPR + t) * VEC;
+        gr[u] = e < ncols ? load16_cached(gamma + e) : u32x4{0u, 0u, 0u, 0u};
       }
-      __syncthreads();
     }
     // Rows are double-buffered in registers: the next row's loads are issued before this
     // row is reduced and written, so HBM reads stay in flight across the reduction, the
@@ -132,7 +142,6 @@ __device__ __forceinline__ void rms_serial(const typename St::T* __restrict__ x,
     };
     if ((i64)blockIdx.x * RPW < rows) fetch((i64)blockIdx.x * RPW);
     for (i64 base = (i64)blockIdx.x * RPW; base < rows; base += step) {
-      asm volatile("" ::: "memory");   // gamma is re-read from LDS for every row
       const i64 row = base + threadIdx.x / TPR;
       const bool live = row < rows;
       const i64 c1 = live ? ncols : 0;
@@ -155,16 +164,43 @@ __device__ __forceinline__ void rms_serial(const typename St::T* __restrict__ x,
       total = row_sum<TPR>(total, lds);
       const float scale = rms_scale<L2>(total, count, eps);
       typename St::T* op = out + (live ? row : 0) * ncols;
+      // L2: the row's elements are divided through div_by_row; a lane holding an element
+      // outside its exact range, or a row whose norm is not finite, stores div_rn results
+      // over them afterwards.
+      const float inv = L2 ? 1.0f / scale : 0.0f;
+      const float tiny = L2 ? __builtin_fmaxf(0x1p-100f, scale * 0x1p-125f) : 0.0f;
+      bool redo = L2 && !(scale <= 0x1.fffffep+127f);
 #pragma unroll
       for (int u = 0; u < NV; ++u) {
         const i64 e = (i64)(u * TPR + t) * VEC;
         if (e >= c1) continue;
         float v[VEC], g[VEC], y[VEC];
         St::unpack(xr[u], v);
-        if constexpr (!L2) St::unpack(gsh[u * TPR + t], g);
+        if constexpr (!L2) St::unpack(gr[u], g);
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) y[j] = rms_readout<St, L2>(v[j], L2 ? 0.0f : g[j], scale);
+        for (int j = 0; j < VEC; ++j) {
+          if constexpr (L2) {
+            y[j] = div_by_row(v[j], scale, inv);
+            redo |= (__builtin_fabsf(v[j]) < tiny) & (v[j] != 0.0f);
+          } else {
+            y[j] = rms_readout<St, L2>(v[j], g[j], scale);
+          }
+        }
         store16(op + e, St::pack(y));
+      }
+      if constexpr (L2) {
+        if (redo) {
+#pragma unroll
+          for (int u = 0; u < NV; ++u) {
+            const i64 e = (i64)(u * TPR + t) * VEC;
+            if (e >= c1) continue;
+            float v[VEC], y[VEC];
+            St::unpack(xr[u], v);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) y[j] = div_rn(v[j], scale);
+            store16(op + e, St::pack(y));
+          }
+        }
       }
     }
   } else {

@@ -197,6 +197,51 @@ def test_rms_l2_against_c_oracle(dtype):
         assert ulps <= 2, ulps
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_l2_division_by_the_row_norm_is_correctly_rounded(dtype):
+    """The L2 readout divides by the row norm through its reciprocal and one exact FMA
+    correction, and hands elements outside that method's exact range to the correctly rounded
+    division: nonzero |v| < 2^-100, quotients below 2^-125 of the norm, rows whose sum of
+    squares overflows.  Rows whose sum of squares is exact in any order (small integers, powers
+    of two) fix the norm, so the output must equal the C oracle's correctly rounded division
+    bit for bit, signed zeros included."""
+    import numpy as np
+
+    from oracle import exact as OX
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(31)
+    w = 4096
+    x = torch.zeros(6, w)
+    x[0] = torch.randint(-7, 8, (w,), generator=g).float()            # integers: exact squares
+    x[0, 10:16] = torch.tensor([2.0 ** -110, -2.0 ** -120, 2.0 ** -126, 0.0, -0.0, 2.0 ** -100])
+    x[1] = torch.randint(-7, 8, (w,), generator=g).float()
+    x[1, 100] = 2.0 ** 100                                             # squares overflow: norm inf
+    x[1, 101] = -3.0
+    x[2, :4] = 2.0 ** 60                                               # norm 2^61
+    x[2, 4:12] = torch.tensor([2.0 ** -80, -2.0 ** -90, 3.0, -5.0, 7.0, 2.0 ** 40, -0.0, 1.0])
+    x[3, 7] = -0.0                                                     # norm 0: divided by eps
+    x[4] = torch.randint(-3, 4, (w,), generator=g).float() * 2.0 ** -60
+    x[5] = torch.randn(w, generator=g)
+    x = x.to(dtype)
+    name = str(dtype).split(".")[1]
+    _say(f"l2 division edge rows {dtype}")
+    got = CG.run_l2_normalize(x.to(dev), eps=1e-6).cpu()
+    want = _from_raw(OX.l2_normalize(_raw(x), name, 1e-6), dtype)
+    view = torch.int16 if dtype != torch.float32 else torch.int32
+    gb, wb = got.view(view), want.view(view)
+    assert torch.equal(gb[:5], wb[:5]), (gb[:5] != wb[:5]).nonzero()[:8].tolist()
+    assert torch.isfinite(got).all()
+    assert (got[1] == 0).all() and bool(torch.signbit(got[1, 101]))   # v / inf = -0 for v < 0
+    assert bool(torch.signbit(got[0, 14])) and bool(torch.signbit(got[3, 7]))
+    # the random row: equal up to the summation order of its norm (one output ulp in bf16;
+    # fp32 keeps that order difference, within the fp32 tolerance)
+    if dtype == torch.float32:
+        torch.testing.assert_close(got[5], want[5], rtol=1e-5, atol=1e-6)
+    else:
+        assert (gb[5].int() - wb[5].int()).abs().max().item() <= 1
+
+
 def test_segment_fused_descriptor_check_matches_reference_asserts():
     """The span checks fused into the segment kernel clear the status word exactly when the
     reference's asserts (range, coverage unless unsafe, monotonic; torch_op.py:378-386, run here
