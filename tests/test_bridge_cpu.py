@@ -55,6 +55,17 @@ def test_split_capacity_golden():
         CG.split_launch_shape(Symbolic(), 1024)
 
 
+def test_two_pass_folds_refuse_the_split_plan():
+    """variance and std carry (mean, M2) over a second pass; the pair merge a split needs is
+    refused for them and the other skeletons compile a split pair."""
+    for name, sk in CG.SKELETONS.items():
+        if sk.two_pass:
+            with pytest.raises(NotImplementedError, match="split refused"):
+                CG.compile_skeleton(name, CG.param_defaults(name), plan="split")
+        else:
+            assert len(CG.compile_skeleton(name, CG.param_defaults(name), plan="split")) == 2
+
+
 def test_operator_identity_golden():
     table = json.loads((GOLDEN / "op_keys.json").read_text())
     for args, want in table["op_key"]:
