@@ -165,11 +165,12 @@ __device__ __forceinline__ void rms_serial(const typename St::T* __restrict__ x,
       const float scale = rms_scale<L2>(total, count, eps);
       typename St::T* op = out + (live ? row : 0) * ncols;
       // L2: the row's elements are divided through div_by_row; a lane holding an element
-      // outside its exact range, or a row whose norm is not finite, stores div_rn results
-      // over them afterwards.
+      // outside its exact range, or a row whose norm (or its reciprocal) is not a normal
+      // number -- an infinite sum of squares, a denormal eps under an underflowed sum, an
+      // eps of 2^126 or more -- stores div_rn results over them afterwards.
       const float inv = L2 ? 1.0f / scale : 0.0f;
       const float tiny = L2 ? __builtin_fmaxf(0x1p-100f, scale * 0x1p-125f) : 0.0f;
-      bool redo = L2 && !(scale <= 0x1.fffffep+127f);
+      bool redo = L2 && !(scale >= 0x1p-126f && scale <= 0x1p126f);
 #pragma unroll
       for (int u = 0; u < NV; ++u) {
         const i64 e = (i64)(u * TPR + t) * VEC;

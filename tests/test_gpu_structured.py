@@ -242,6 +242,32 @@ def test_l2_division_by_the_row_norm_is_correctly_rounded(dtype):
         assert (gb[5].int() - wb[5].int()).abs().max().item() <= 1
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_l2_norm_whose_reciprocal_is_not_normal_takes_the_exact_division(dtype):
+    """eps is any finite positive number: a denormal eps under a row whose squares all
+    underflow (norm = eps = 1e-40, reciprocal overflows), and eps >= 2^126 (reciprocal
+    denormal).  The fast reciprocal path does not hold there; the rows must still equal the
+    C oracle's correctly rounded division bit for bit."""
+    from oracle import exact as OX
+
+    dev = _dev()
+    name = str(dtype).split(".")[1]
+    view = torch.int16 if dtype != torch.float32 else torch.int32
+    w = 512
+    tiny_row = torch.zeros(2, w)
+    tiny_row[0, ::3] = 2.0 ** -90                   # squares 2^-180 underflow to 0
+    tiny_row[0, 1::7] = -(2.0 ** -80)
+    tiny_row[1, 5] = 2.0 ** -75
+    big_eps_rows = torch.randint(-40, 41, (2, w), generator=torch.Generator().manual_seed(33)).float()
+    for x, eps in ((tiny_row, 1e-40), (big_eps_rows, 1e38), (big_eps_rows * 2.0 ** 50, 2.0 ** 127)):
+        x = x.to(dtype)
+        _say(f"l2 eps={eps} {dtype}")
+        got = CG.run_l2_normalize(x.to(dev), eps=eps).cpu()
+        want = _from_raw(OX.l2_normalize(_raw(x), name, eps), dtype)
+        assert torch.isfinite(got).all()
+        assert torch.equal(got.view(view), want.view(view)), (got.view(view) != want.view(view)).nonzero()[:8].tolist()
+
+
 def test_segment_fused_descriptor_check_matches_reference_asserts():
     """The span checks fused into the segment kernel clear the status word exactly when the
     reference's asserts (range, coverage unless unsafe, monotonic; torch_op.py:378-386, run here
