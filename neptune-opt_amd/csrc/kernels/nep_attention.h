@@ -361,7 +361,8 @@ __device__ void attention_exact_rows(const T* __restrict__ qp, const T* __restri
           for (int d = 0; d < DQ; ++d) ov[d] *= alpha;
           m = s;
         }
-        const float p = __builtin_amdgcn_exp2f(s - m);
+        // m is still -inf only while every score seen is -inf: those add nothing
+        const float p = m == -kInf ? 0.0f : __builtin_amdgcn_exp2f(s - m);
         l += p;
 #pragma unroll
         for (int i = 0; i < DQ / 8; ++i)
@@ -611,7 +612,8 @@ __device__ __forceinline__ void attention_fwd(const T* __restrict__ q, const T* 
   // ---- readout: O / l, and the natural-log LSE of the scaled scores
   const float l_lane = l_even + l_odd;
   const float l_tot = l_lane + partner<32>(l_lane);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  // l_tot is 0 only for a row whose visible scores are all -inf: 0 * inf = NaN, as softmax
+  const float inv = 1.0f / l_tot;
   if (my_q < sq) {
     T* orow = orow0 + (i64)my_q * D;
 #pragma unroll

@@ -262,6 +262,31 @@ def test_attention_non_finite_v_reaches_only_the_rows_that_see_it(value, causal)
     torch.testing.assert_close(lse.cpu(), _lse_reference(q, k, causal), rtol=LSE_RTOL, atol=LSE_ATOL)
 
 
+@pytest.mark.parametrize("exact", [False, True])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_rows_whose_scores_are_all_minus_inf(causal, exact):
+    """A query holding -inf against keys that are all positive in that dimension scores -inf on
+    every key: softmax gives NaN for the row and logsumexp -inf, on the MFMA path and on the
+    exact path alike; the other rows are unaffected."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(20)
+    B, H, S, D = 1, 2, 200, 128
+    q, k, v = (torch.randn(B, H, S, D, generator=g) for _ in range(3))
+    k[..., 3] = k[..., 3].abs() + 0.5
+    q[0, 1, 150, 3] = float("-inf")
+    q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    _say(f"attention all -inf row causal={causal} exact={exact}")
+    out, lse, _ = A._launch(q.to(dev), k.to(dev), v.to(dev), None, causal, True, -1 if exact else 13)
+    got, lse = out.cpu().float(), lse.cpu()
+    assert torch.isnan(got[0, 1, 150]).all()
+    assert lse[0, 1, 150] == float("-inf")
+    want = R.attention_reference(q, k, v, causal=causal).float()
+    keep = torch.ones(B, H, S, dtype=torch.bool)
+    keep[0, 1, 150] = False
+    torch.testing.assert_close(got[keep], want[keep], rtol=1.6e-2, atol=1e-3)
+    torch.testing.assert_close(lse[keep], _lse_reference(q, k, causal)[keep], rtol=LSE_RTOL, atol=LSE_ATOL)
+
+
 def test_attention_strided_layout_and_scale():
     """[B, S, H, D] storage viewed as [B, H, S, D] (the common projection layout)."""
     dev = _dev()
