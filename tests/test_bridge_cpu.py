@@ -60,7 +60,7 @@ def test_two_pass_folds_refuse_the_split_plan():
     refused for them and the other skeletons compile a split pair."""
     for name, sk in CG.SKELETONS.items():
         if sk.two_pass:
-            with pytest.raises(NotImplementedError, match="split refused"):
+            with pytest.raises(NotImplementedError, match="two_pass needs extended carried state"):
                 CG.compile_skeleton(name, CG.param_defaults(name), plan="split")
         else:
             assert len(CG.compile_skeleton(name, CG.param_defaults(name), plan="split")) == 2

@@ -76,7 +76,7 @@ def test_every_skeleton_every_dtype(name, dtype, plan):
     if plan == "split" and sk.two_pass:
         # a split needs the pair merge, which two-pass folds refuse (their carried state
         # would need the second pass's inputs); the run raises before any launch
-        with pytest.raises(NotImplementedError, match="split refused"):
+        with pytest.raises(NotImplementedError, match="two_pass needs extended carried state"):
             CG.run(name, torch.ones(4, 8, dtype=dtype, device=dev), plan="split", block=256)
         return
     g = torch.Generator().manual_seed(7)
