@@ -271,12 +271,81 @@ def per_fold(dev, xs_cpu, xs_dev, cpu: bool = True):
         "bf16_gemm_TFLOP_s": round(gemm, 1), "frac_of_bf16_gemm": round(tflops / gemm, 4),
         "rocprof_pmc": attention_pmc()}
     log(f"[bench] cfg5 attention: {folds[key5]}")
+    folds["reference_shapes"] = reference_shapes(dev)
     qh, kh, vh = (t[0:1, 0:2] for t in qkv)
     beside(key5, "cfg5 attention", lambda: R.attention_reference(qh, kh, vh, causal=True),
            flops / 64 / 1e12, "TFLOP/s",
            "heads (0,0) and (0,1) of 128, i.e. 1/64 of the FLOPs, scaled linearly to the whole "
            "job; fp32 softmax(scale*QK^T + causal) V (SDPA math form)")
     return folds
+
+
+# The reference's own published latencies for this path (RTX 5090 D v2, torch 2.11 + Triton
+# 3.6; README.md and docs/evidence/ of the reference): context beside this build's time at the
+# same shapes, not a same-hardware comparison.
+REFERENCE_SHAPES = (
+    ("logsumexp_f32_256x16384", "logsumexp", (256, 16384), "float32", "serial", 18.3,
+     "README.md:243; docs/evidence/exp33_real_modules_gpu.txt:30"),
+    ("stable_l2_f32_256x16384", "stable_l2", (256, 16384), "float32", "serial", 18.4,
+     "docs/evidence/exp33_real_modules_gpu.txt:38"),
+    ("logsumexp_f32_256x262144", "logsumexp", (256, 262144), "float32", "serial", 214.0,
+     "docs/evidence/exp37_autotune_gpu.txt:89"),
+    ("logsumexp_f32_4096x4096", "logsumexp", (4096, 4096), "float32", "serial", 12.4,
+     "docs/evidence/exp37_autotune_gpu.txt:208"),
+    ("logsumexp_f32_1x262144_split", "logsumexp", (1, 262144), "float32", "split", 12.58,
+     "README.md:205-210"),
+    ("rms_norm_f32_1x65536_split", "rms_norm", (1, 65536), "float32", "split", 10.25,
+     "README.md:190-191"),
+    ("rms_norm_bf16_1125x512", "rms_norm", (1125, 512), "bfloat16", "serial", 9.10,
+     "README.md:192-193"),
+    ("segment_mean_bf16_4096x64_64segments", "segment_mean", (4096, 64), "bfloat16", "serial",
+     101.85, "README.md:194-195"),
+)
+
+
+def reference_shapes(dev):
+    """This build at the shapes the reference publishes latencies for: the device time per
+    call (graph replay, inputs rotated as for the configs) and the eager time per call (events
+    around 200 back-to-back Python calls: launch and host overhead included)."""
+    import torch
+
+    import neptune_codegen as CG
+
+    out = {}
+    for key, name, shape, dtype, plan, published, source in REFERENCE_SHAPES:
+        dt = getattr(torch, dtype)
+        x0 = torch.randn(*shape, generator=seeded(21)).to(dt).to(dev)
+        if name == "rms_norm":
+            gamma = torch.ones(shape[1], dtype=dt, device=dev)
+
+            def call(y, gamma=gamma, plan=plan):
+                return CG.run_rms_norm(y, gamma, eps=1e-6, plan=plan)
+        elif name == "segment_mean":
+            offsets = torch.arange(0, shape[0] + 1, shape[0] // 64, dtype=torch.int64, device=dev)
+
+            def call(y, offsets=offsets):
+                return CG.run_segment_pool(y, offsets, reduce="mean", offsets=True)
+        else:
+            def call(y, name=name, plan=plan):
+                return CG.run(name, y, plan=plan)
+        n = copies_for(x0.numel() * x0.element_size())
+        xs = [x0] + [x0.clone() for _ in range(n - 1)]
+        ms = graph_time(lambda i: call(xs[i % n]), replays=5, inner=max(20, n))
+        for _ in range(20):
+            call(x0)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(200):
+            call(x0)
+        end.record()
+        torch.cuda.synchronize()
+        eager_us = start.elapsed_time(end) / 200 * 1e3
+        out[key] = {"us": round(ms * 1e3, 2), "eager_us": round(eager_us, 2), "plan": plan,
+                    "published_us": published, "published_hw": "RTX 5090 D v2",
+                    "source": f"reference {source}"}
+        log(f"[bench] reference shape {key}: {out[key]}")
+    return out
 
 
 class CpuHost:

@@ -232,8 +232,29 @@ def _parameter_substitutions(sk, values: dict | None) -> dict:
     return out
 
 
+_MERGE_CERTIFICATES: dict = {}
+
+
 def derive_merge_certificate(sk, values: dict | None = None) -> MergeCertificate:
-    """Prove the repair, its cocycle and identity exactly before partial states may merge."""
+    """Prove the repair, its cocycle and identity exactly before partial states may merge.
+
+    The proof is a pure function of the skeleton and its parameter values and takes about a
+    millisecond of symbolic simplification, so a proved certificate is kept per (skeleton,
+    values) -- values keyed by type and repr, so 1 and 1.0, 0.0 and -0.0 stay distinct -- and
+    every split call after the first reuses it.  A refused pair is proved (and refused) again."""
+    try:
+        key = (sk, tuple(sorted((k, type(v).__name__, repr(v)) for k, v in (values or {}).items())))
+        hash(key)
+    except TypeError:
+        return _prove_merge_certificate(sk, values)
+    cert = _MERGE_CERTIFICATES.get(key)
+    if cert is None:
+        cert = _prove_merge_certificate(sk, values)
+        _MERGE_CERTIFICATES[key] = cert
+    return cert
+
+
+def _prove_merge_certificate(sk, values: dict | None) -> MergeCertificate:
     if sk.two_pass:
         raise NotImplementedError("two_pass needs extended carried state; pair merge refused")
     if sk.producer_reducer not in ("max", "sum"):

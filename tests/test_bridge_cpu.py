@@ -66,6 +66,28 @@ def test_two_pass_folds_refuse_the_split_plan():
             assert len(CG.compile_skeleton(name, CG.param_defaults(name), plan="split")) == 2
 
 
+def test_split_certificate_and_structured_programs_are_reused_per_parameter_set():
+    """The merge certificate (a symbolic proof, ~1 ms) and the structured program are kept per
+    exact parameter set: a repeated call gets the same object, a value of another type or sign
+    is proved and validated afresh, and refusals are raised every time."""
+    from neptune_codegen.algebra import derive_merge_certificate
+
+    sk = CG.SKELETONS["softcap_lse"]
+    a = derive_merge_certificate(sk, {"beta": 1.0, "tiny": 0.0})
+    assert derive_merge_certificate(sk, {"tiny": 0.0, "beta": 1.0}) is a
+    assert derive_merge_certificate(sk, {"beta": 1.0, "tiny": -0.0}) is not a
+    assert derive_merge_certificate(sk, {"beta": 1, "tiny": 0.0}) is not a
+    for _ in range(2):
+        with pytest.raises(NotImplementedError, match="two_pass"):
+            derive_merge_certificate(CG.SKELETONS["variance"], {})
+    prog = T.compile_state_reduction("rms_norm", {"eps": 0.5})
+    assert T.compile_state_reduction("rms_norm", {"eps": 0.5}) is prog
+    for bad in ({"eps": True}, {"eps": "0.5"}, {"eps": 0.0}, {"eps": 0.5, "extra": 1}):
+        for _ in range(2):
+            with pytest.raises(ValueError):
+                T.compile_state_reduction("rms_norm", bad)
+
+
 def test_operator_identity_golden():
     table = json.loads((GOLDEN / "op_keys.json").read_text())
     for args, want in table["op_key"]:
