@@ -324,9 +324,10 @@ def launch_reduction(kernel, plan, x2, out, rows, ncols, block, num_warps, *, wr
                             heavy_phi=kernel.heavy_phi)
         k = kernel.kernel(var, "", device)
         rpw = max(1, var.wg // var.tpr)
-        k.launch((_grid_1d(rows, rpw),),
-                 (x2.data_ptr(), out.data_ptr(), rows, ncols, x2.stride(0), x2.stride(1)), stream)
-        return
+        grid = (_grid_1d(rows, rpw),)
+        tail = (rows, ncols, x2.stride(0), x2.stride(1))
+        k.launch(grid, (x2.data_ptr(), out.data_ptr()) + tail, stream)
+        return k, grid, tail
     nparts, _merge = split_launch_shape(ncols, block)
     partial_m = hip.scratch(torch.empty((rows, nparts), device=x2.device, dtype=torch.float32))
     partial_a = hip.scratch(torch.empty((rows, nparts), device=x2.device, dtype=torch.float32))
@@ -346,6 +347,10 @@ def launch_reduction(kernel, plan, x2, out, rows, ncols, block, num_warps, *, wr
                partial_s.data_ptr(), out.data_ptr(), rows, ncols, nparts), stream)
 
 
+_RUN_SEEN: dict = {}
+_RUN_SEEN_MAX = 4096
+
+
 def run(name: str, x, block: int | None = None, num_warps: int | None = None,
         keepdim: bool = False, plan: str = "serial", **params):
     """Reduce the last dimension of `x` with the generated fold `name`.
@@ -353,12 +358,31 @@ def run(name: str, x, block: int | None = None, num_warps: int | None = None,
     Rank >= 1 returns x.shape[:-1] (keepdim appends a 1).  Real execution needs a ROCm device
     and float16/bfloat16/float32; Fake/meta tensors return metadata only.  Declared parameter
     defaults are filled for anything not passed.
+
+    A serial call on a plain device tensor whose (fold, dtype, device, shape, strides, 16-byte
+    alignment, launch options, parameter types and values) were seen before reuses that call's
+    kernel and launch shape: everything the validation and the launch choice read is in that
+    key, so only the output allocation and the launch remain.
     """
     import torch
     from torch._subclasses.fake_tensor import FakeTensor
 
     from neptune_codegen.skeleton import param_defaults
 
+    seen = None
+    if plan == "serial" and type(x) is torch.Tensor and x.is_cuda:
+        try:
+            seen = (name, x.dtype, x.device, tuple(x.shape), tuple(x.stride()), x.data_ptr() % 16,
+                    block, num_warps, keepdim,
+                    tuple(sorted((k, type(v).__name__, repr(v)) for k, v in params.items())))
+            entry = _RUN_SEEN.get(seen)
+        except TypeError:
+            seen, entry = None, None
+        if entry is not None:
+            kern, grid, out_shape, tail = entry
+            out = torch.empty(out_shape, device=x.device, dtype=x.dtype)
+            kern.launch(grid, (x.data_ptr(), out.data_ptr()) + tail, hip.current_stream(x.device))
+            return out
     metadata = isinstance(x, FakeTensor) or x.device.type == "meta"
     _validate_row_last(x, metadata=metadata)
     params = {**param_defaults(name), **(params or {})}
@@ -382,7 +406,11 @@ def run(name: str, x, block: int | None = None, num_warps: int | None = None,
         cfg = best_config(rows, ncols, x.dtype, x.device)
         block = cfg[0] if block is None else block
         num_warps = cfg[1] if num_warps is None else num_warps
-    launch_reduction(kernel, plan, x2, out, rows, ncols, block, num_warps)
+    launch = launch_reduction(kernel, plan, x2, out, rows, ncols, block, num_warps)
+    if seen is not None and launch is not None and x2.data_ptr() == x.data_ptr():
+        if len(_RUN_SEEN) >= _RUN_SEEN_MAX:
+            _RUN_SEEN.clear()
+        _RUN_SEEN[seen] = (launch[0], launch[1], tuple(out.shape), launch[2])
     return out
 
 

@@ -172,6 +172,27 @@ def test_wide_rows_at_default_shapes(name, dtype):
         torch.testing.assert_close(got.cpu().float(), want.to(dtype).float(), rtol=rtol, atol=atol)
 
 
+def test_repeated_calls_reuse_their_launch_and_stay_exact():
+    """A repeated serial call reuses the first call's kernel and launch shape: calls that
+    differ in alignment, strides, keepdim or a parameter value must not share it."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(23)
+    base = torch.randn(64, 1001, generator=g).bfloat16()
+    xd = base.to(dev)
+    views = [xd[:, :1000], xd[:, 1:], xd[:, :1000], xd[:, 1:]]   # 16-byte aligned, then not
+    for view in views:
+        _say(f"repeated call, offset {view.storage_offset()}")
+        got = CG.run("logsumexp", view)
+        torch.testing.assert_close(got.cpu().float(), R.reference("logsumexp", view.cpu()).bfloat16().float(),
+                                   rtol=torch.finfo(torch.bfloat16).eps, atol=1e-5)
+    kept = CG.run("logsumexp", views[0], keepdim=True)
+    assert kept.shape == (64, 1)
+    xs = torch.randn(32, 512, generator=g)
+    for beta in (1.0, 2.0, 1.0):
+        got = CG.run("softcap_lse", xs.to(dev), beta=beta)
+        torch.testing.assert_close(got.cpu(), R.reference("softcap_lse", xs, beta=beta), rtol=1e-5, atol=1e-6)
+
+
 def test_strided_views_and_keepdim():
     dev = _dev()
     g = torch.Generator().manual_seed(3)
