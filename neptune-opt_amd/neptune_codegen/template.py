@@ -573,10 +573,10 @@ def launch_rms_norm(kernel, x, gamma, out, *, plan="serial", wrapper=None):
         var = _row_variant(flat, gamma, width)
         (k,) = kernel.kernels(var, device)
         rpw = max(1, var.wg // var.tpr)
-        k.launch((_persistent_grid(rpw, rows, x.device),),
-                 (flat.data_ptr(), g_ptr, out.data_ptr(), rows, width, flat.stride(0),
-                  flat.stride(1), g_stride), stream)
-        return
+        grid = (_persistent_grid(rpw, rows, x.device),)
+        tail = (rows, width, flat.stride(0), flat.stride(1), g_stride)
+        k.launch(grid, (flat.data_ptr(), g_ptr, out.data_ptr()) + tail, stream)
+        return (k, grid, tail) if flat.data_ptr() == x.data_ptr() else None
     parts, _ = split_launch_shape(width, 1024)
     totals = hip.scratch(torch.empty((rows, parts), device=x.device, dtype=torch.float32))
     counts = hip.scratch(torch.empty((rows, parts), device=x.device, dtype=torch.int64))
@@ -591,33 +591,72 @@ def launch_rms_norm(kernel, x, gamma, out, *, plan="serial", wrapper=None):
                         parts, 1024), stream)
 
 
-def run_rms_norm(x, gamma, *, eps: float = 1e-6, plan="serial"):
-    """Full-vector RMSNorm over the last dimension; fresh contiguous output in x.dtype."""
+_ROW_SEEN: dict = {}
+
+
+def _row_seen_key(name, x, gamma, eps, plan):
+    """Key of a serial RMS / L2 call on plain device tensors: everything the validation and the
+    launch choice read (dtypes, devices, shapes, strides, 16-byte alignment, eps's type and
+    value); None when the call takes the full path."""
+    import torch
+
+    if plan != "serial" or type(x) is not torch.Tensor or not x.is_cuda:
+        return None
+    if gamma is None:
+        g = None
+    elif type(gamma) is torch.Tensor:
+        g = (gamma.dtype, gamma.device, gamma.layout, tuple(gamma.shape), tuple(gamma.stride()),
+             gamma.data_ptr() % 16)
+    else:
+        return None
+    try:
+        key = (name, x.dtype, x.device, tuple(x.shape), tuple(x.stride()), x.data_ptr() % 16, g,
+               type(eps).__name__, repr(eps))
+        hash(key)
+    except TypeError:
+        return None
+    return key
+
+
+def _row_run(name, x, gamma, eps, plan, validate):
     import torch
     from torch._subclasses.fake_tensor import FakeTensor
 
+    key = _row_seen_key(name, x, gamma, eps, plan)
+    entry = _ROW_SEEN.get(key) if key is not None else None
+    if entry is not None:
+        k, grid, tail = entry
+        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+        k.launch(grid, (x.data_ptr(), gamma.data_ptr() if gamma is not None else 0,
+                        out.data_ptr()) + tail, hip.current_stream(x.device))
+        return out
     params = {"eps": eps}
     metadata = isinstance(x, FakeTensor) or x.device.type == "meta"
-    shape = validate_rms_inputs(x, gamma, params, plan=plan, metadata=metadata)
+    shape = validate(params, metadata)
     out = torch.empty(shape, device=x.device, dtype=x.dtype)
     if metadata or x.numel() == 0:
         return out
-    kernel = compile_state_reduction("rms_norm", params, plan=plan)
-    launch_rms_norm(kernel, x, gamma, out, plan=plan)
+    kernel = compile_state_reduction(name, params, plan=plan)
+    launch = launch_rms_norm(kernel, x, gamma, out, plan=plan)
+    if key is not None and launch is not None:
+        if len(_ROW_SEEN) >= _RUN_SEEN_MAX:
+            _ROW_SEEN.clear()
+        _ROW_SEEN[key] = launch
     return out
+
+
+def run_rms_norm(x, gamma, *, eps: float = 1e-6, plan="serial"):
+    """Full-vector RMSNorm over the last dimension; fresh contiguous output in x.dtype.  A
+    serial call whose tensors and eps match an earlier call's (dtypes, devices, shapes,
+    strides, alignment, eps's type and value) reuses that call's kernel and launch shape."""
+    return _row_run("rms_norm", x, gamma, eps, plan,
+                    lambda params, metadata: validate_rms_inputs(x, gamma, params, plan=plan,
+                                                                 metadata=metadata))
 
 
 def run_l2_normalize(x, *, eps: float = 1e-6, plan="serial"):
-    """x / max(||x||_2, eps) over the last dimension (fp32 statistics, dtype output)."""
-    import torch
-    from torch._subclasses.fake_tensor import FakeTensor
-
-    params = {"eps": eps}
-    metadata = isinstance(x, FakeTensor) or x.device.type == "meta"
-    shape = validate_l2_inputs(x, params, plan=plan, metadata=metadata)
-    out = torch.empty(shape, device=x.device, dtype=x.dtype)
-    if metadata or x.numel() == 0:
-        return out
-    kernel = compile_state_reduction("l2_normalize", params, plan=plan)
-    launch_rms_norm(kernel, x, None, out, plan=plan)
-    return out
+    """x / max(||x||_2, eps) over the last dimension (fp32 statistics, dtype output); repeated
+    serial calls reuse their launch as run_rms_norm's do."""
+    return _row_run("l2_normalize", x, None, eps, plan,
+                    lambda params, metadata: validate_l2_inputs(x, params, plan=plan,
+                                                                metadata=metadata))

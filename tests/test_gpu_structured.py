@@ -53,6 +53,32 @@ def test_rms_norm_parity(dtype, plan):
         torch.testing.assert_close(got.cpu().float(), want.float(), rtol=rtol, atol=atol)
 
 
+def test_repeated_rms_and_l2_calls_reuse_their_launch_and_stay_exact():
+    """Repeated serial RMSNorm / L2 calls reuse the first call's kernel and launch shape; calls
+    that differ in gamma's alignment or stride, x's alignment, or eps must not share it."""
+    from oracle import exact as OX
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(24)
+    x = torch.randn(40, 520, generator=g).bfloat16()
+    gam = (1 + 0.1 * torch.randn(2 * 520 + 8, generator=g)).bfloat16()
+    xd, gd = x.to(dev), gam.to(dev)
+    xs = [xd[:, :512], xd[:, 8:], xd[:, :512], xd[:, 1:513]]
+    gammas = [gd[:512], gd[8:520], gd[1:513], gd[:1024:2]]
+    for eps in (1e-6, 1e-2, 1e-6):
+        for xv in xs:
+            for gv in gammas:
+                _say(f"rms repeated x+{xv.storage_offset()} gamma+{gv.storage_offset()}/{gv.stride(0)} eps={eps}")
+                got = CG.run_rms_norm(xv, gv, eps=eps).cpu()
+                want = _from_raw(OX.rms_norm(_raw(xv.cpu().contiguous()), _raw(gv.cpu().contiguous()),
+                                             "bfloat16", eps), torch.bfloat16)
+                diff = (got.view(torch.int16).int() - want.view(torch.int16).int()).abs().max().item()
+                assert diff <= 2, (eps, xv.storage_offset(), gv.storage_offset(), diff)
+            got = CG.run_l2_normalize(xv, eps=eps).cpu()
+            want = _from_raw(OX.l2_normalize(_raw(xv.cpu().contiguous()), "bfloat16", eps), torch.bfloat16)
+            assert (got.view(torch.int16).int() - want.view(torch.int16).int()).abs().max().item() <= 1
+
+
 def test_rms_cfg3_shape_and_strided_gamma():
     dev = _dev()
     g = torch.Generator().manual_seed(3)
