@@ -229,6 +229,11 @@ class recording:
         _recording.active = self._previous
 
 
+def recording_active() -> bool:
+    """Whether this thread records launches (hip.recording())."""
+    return getattr(_recording, "active", None) is not None
+
+
 def scratch(tensor):
     """Mark a tensor allocated by a launch path as per-call scratch (recorded when active)."""
     recorder = getattr(_recording, "active", None)

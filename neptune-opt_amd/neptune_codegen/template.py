@@ -337,14 +337,15 @@ def launch_reduction(kernel, plan, x2, out, rows, ncols, block, num_warps, *, wr
     var = _fold_variant(x2, ncols, block, num_warps, split_block=block)
     kp = partial.kernel(var, "partial", device)
     rpw = max(1, var.wg // var.tpr)
-    kp.launch((_grid_1d(rows * nparts, rpw),),
-              (x2.data_ptr(), partial_m.data_ptr(), partial_a.data_ptr(), partial_v.data_ptr(),
-               partial_s.data_ptr(), rows, ncols, x2.stride(0), x2.stride(1), nparts, block),
-              stream)
+    grid_p, grid_m = (_grid_1d(rows * nparts, rpw),), (_grid_1d(rows, 4),)
+    tail_p = (rows, ncols, x2.stride(0), x2.stride(1), nparts, block)
+    tail_m = (rows, ncols, nparts)
+    kp.launch(grid_p, (x2.data_ptr(), partial_m.data_ptr(), partial_a.data_ptr(),
+                       partial_v.data_ptr(), partial_s.data_ptr()) + tail_p, stream)
     km = merge.kernel(var, "merge", device)
-    km.launch((_grid_1d(rows, 4),),
-              (partial_m.data_ptr(), partial_a.data_ptr(), partial_v.data_ptr(),
-               partial_s.data_ptr(), out.data_ptr(), rows, ncols, nparts), stream)
+    km.launch(grid_m, (partial_m.data_ptr(), partial_a.data_ptr(), partial_v.data_ptr(),
+                       partial_s.data_ptr(), out.data_ptr()) + tail_m, stream)
+    return kp, grid_p, tail_p, km, grid_m, tail_m, rows * nparts
 
 
 _RUN_SEEN: dict = {}
@@ -359,10 +360,10 @@ def run(name: str, x, block: int | None = None, num_warps: int | None = None,
     and float16/bfloat16/float32; Fake/meta tensors return metadata only.  Declared parameter
     defaults are filled for anything not passed.
 
-    A serial call on a plain device tensor whose (fold, dtype, device, shape, strides, 16-byte
+    A call on a plain device tensor whose (fold, plan, dtype, device, shape, strides, 16-byte
     alignment, launch options, parameter types and values) were seen before reuses that call's
-    kernel and launch shape: everything the validation and the launch choice read is in that
-    key, so only the output allocation and the launch remain.
+    kernels and launch shapes: everything the validation and the launch choice read is in that
+    key, so only the allocations and the launches remain (not while launches are recorded).
     """
     import torch
     from torch._subclasses.fake_tensor import FakeTensor
@@ -370,18 +371,28 @@ def run(name: str, x, block: int | None = None, num_warps: int | None = None,
     from neptune_codegen.skeleton import param_defaults
 
     seen = None
-    if plan == "serial" and type(x) is torch.Tensor and x.is_cuda:
+    if type(x) is torch.Tensor and x.is_cuda and not hip.recording_active():
         try:
-            seen = (name, x.dtype, x.device, tuple(x.shape), tuple(x.stride()), x.data_ptr() % 16,
-                    block, num_warps, keepdim,
+            seen = (name, plan, x.dtype, x.device, tuple(x.shape), tuple(x.stride()),
+                    x.data_ptr() % 16, block, num_warps, keepdim,
                     tuple(sorted((k, type(v).__name__, repr(v)) for k, v in params.items())))
             entry = _RUN_SEEN.get(seen)
         except TypeError:
             seen, entry = None, None
         if entry is not None:
-            kern, grid, out_shape, tail = entry
-            out = torch.empty(out_shape, device=x.device, dtype=x.dtype)
-            kern.launch(grid, (x.data_ptr(), out.data_ptr()) + tail, hip.current_stream(x.device))
+            out = torch.empty(entry[0], device=x.device, dtype=x.dtype)
+            stream = hip.current_stream(x.device)
+            if plan == "serial":
+                _, kern, grid, tail = entry
+                kern.launch(grid, (x.data_ptr(), out.data_ptr()) + tail, stream)
+                return out
+            _, kp, grid_p, tail_p, km, grid_m, tail_m, count = entry
+            # one allocation holds the four partial arrays (m, acc: fp32; seen, status: int32)
+            parts = torch.empty(4 * count, device=x.device, dtype=torch.float32)
+            base = parts.data_ptr()
+            ptrs = (base, base + 4 * count, base + 8 * count, base + 12 * count)
+            kp.launch(grid_p, (x.data_ptr(),) + ptrs + tail_p, stream)
+            km.launch(grid_m, ptrs + (out.data_ptr(),) + tail_m, stream)
             return out
     metadata = isinstance(x, FakeTensor) or x.device.type == "meta"
     _validate_row_last(x, metadata=metadata)
@@ -410,7 +421,7 @@ def run(name: str, x, block: int | None = None, num_warps: int | None = None,
     if seen is not None and launch is not None and x2.data_ptr() == x.data_ptr():
         if len(_RUN_SEEN) >= _RUN_SEEN_MAX:
             _RUN_SEEN.clear()
-        _RUN_SEEN[seen] = (launch[0], launch[1], tuple(out.shape), launch[2])
+        _RUN_SEEN[seen] = (tuple(out.shape),) + tuple(launch)
     return out
 
 
@@ -600,7 +611,7 @@ def _row_seen_key(name, x, gamma, eps, plan):
     value); None when the call takes the full path."""
     import torch
 
-    if plan != "serial" or type(x) is not torch.Tensor or not x.is_cuda:
+    if plan != "serial" or type(x) is not torch.Tensor or not x.is_cuda or hip.recording_active():
         return None
     if gamma is None:
         g = None

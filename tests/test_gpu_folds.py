@@ -191,6 +191,14 @@ def test_repeated_calls_reuse_their_launch_and_stay_exact():
     for beta in (1.0, 2.0, 1.0):
         got = CG.run("softcap_lse", xs.to(dev), beta=beta)
         torch.testing.assert_close(got.cpu(), R.reference("softcap_lse", xs, beta=beta), rtol=1e-5, atol=1e-6)
+    # the split plan: the repeated call puts the four partial arrays in one allocation
+    xw = torch.randn(3, 40000, generator=g)
+    want = R.reference("logsumexp", xw)
+    first = CG.run("logsumexp", xw.to(dev), plan="split")
+    for _ in range(3):
+        again = CG.run("logsumexp", xw.to(dev), plan="split")
+        assert torch.equal(again, first)
+    torch.testing.assert_close(first.cpu(), want, rtol=1e-5, atol=1e-6)
 
 
 def test_strided_views_and_keepdim():
