@@ -594,24 +594,27 @@ def launch_rms_norm(kernel, x, gamma, out, *, plan="serial", wrapper=None):
     var = _row_variant(flat, gamma, width, tile=1024)
     kp, km = kernel.kernels(var, device)
     rpw = max(1, var.wg // var.tpr)
-    grid = _persistent_grid(rpw, rows * parts, x.device)
-    kp.launch((grid,), (flat.data_ptr(), totals.data_ptr(), counts.data_ptr(), rows, width,
-                        flat.stride(0), flat.stride(1), parts, 1024), stream)
-    km.launch((grid,), (flat.data_ptr(), g_ptr, totals.data_ptr(), counts.data_ptr(),
-                        out.data_ptr(), rows, width, flat.stride(0), flat.stride(1), g_stride,
-                        parts, 1024), stream)
+    grid = (_persistent_grid(rpw, rows * parts, x.device),)
+    tail_p = (rows, width, flat.stride(0), flat.stride(1), parts, 1024)
+    tail_m = (rows, width, flat.stride(0), flat.stride(1), g_stride, parts, 1024)
+    kp.launch(grid, (flat.data_ptr(), totals.data_ptr(), counts.data_ptr()) + tail_p, stream)
+    km.launch(grid, (flat.data_ptr(), g_ptr, totals.data_ptr(), counts.data_ptr(),
+                     out.data_ptr()) + tail_m, stream)
+    if flat.data_ptr() != x.data_ptr():
+        return None
+    return kp, km, grid, tail_p, tail_m, rows * parts
 
 
 _ROW_SEEN: dict = {}
 
 
 def _row_seen_key(name, x, gamma, eps, plan):
-    """Key of a serial RMS / L2 call on plain device tensors: everything the validation and the
-    launch choice read (dtypes, devices, shapes, strides, 16-byte alignment, eps's type and
-    value); None when the call takes the full path."""
+    """Key of an RMS / L2 call on plain device tensors: everything the validation and the
+    launch choice read (plan, dtypes, devices, shapes, strides, 16-byte alignment, eps's type
+    and value); None when the call takes the full path."""
     import torch
 
-    if plan != "serial" or type(x) is not torch.Tensor or not x.is_cuda or hip.recording_active():
+    if type(x) is not torch.Tensor or not x.is_cuda or hip.recording_active():
         return None
     if gamma is None:
         g = None
@@ -621,8 +624,8 @@ def _row_seen_key(name, x, gamma, eps, plan):
     else:
         return None
     try:
-        key = (name, x.dtype, x.device, tuple(x.shape), tuple(x.stride()), x.data_ptr() % 16, g,
-               type(eps).__name__, repr(eps))
+        key = (name, plan, x.dtype, x.device, tuple(x.shape), tuple(x.stride()),
+               x.data_ptr() % 16, g, type(eps).__name__, repr(eps))
         hash(key)
     except TypeError:
         return None
@@ -636,10 +639,19 @@ def _row_run(name, x, gamma, eps, plan, validate):
     key = _row_seen_key(name, x, gamma, eps, plan)
     entry = _ROW_SEEN.get(key) if key is not None else None
     if entry is not None:
-        k, grid, tail = entry
         out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
-        k.launch(grid, (x.data_ptr(), gamma.data_ptr() if gamma is not None else 0,
-                        out.data_ptr()) + tail, hip.current_stream(x.device))
+        g_ptr = gamma.data_ptr() if gamma is not None else 0
+        stream = hip.current_stream(x.device)
+        if plan == "serial":
+            k, grid, tail = entry
+            k.launch(grid, (x.data_ptr(), g_ptr, out.data_ptr()) + tail, stream)
+            return out
+        kp, km, grid, tail_p, tail_m, count = entry
+        # one allocation: the int64 counts, then the fp32 totals
+        scratch = torch.empty((3 * count + 1) // 2, device=x.device, dtype=torch.int64)
+        counts, totals = scratch.data_ptr(), scratch.data_ptr() + 8 * count
+        kp.launch(grid, (x.data_ptr(), totals, counts) + tail_p, stream)
+        km.launch(grid, (x.data_ptr(), g_ptr, totals, counts, out.data_ptr()) + tail_m, stream)
         return out
     params = {"eps": eps}
     metadata = isinstance(x, FakeTensor) or x.device.type == "meta"

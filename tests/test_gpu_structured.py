@@ -77,6 +77,14 @@ def test_repeated_rms_and_l2_calls_reuse_their_launch_and_stay_exact():
             got = CG.run_l2_normalize(xv, eps=eps).cpu()
             want = _from_raw(OX.l2_normalize(_raw(xv.cpu().contiguous()), "bfloat16", eps), torch.bfloat16)
             assert (got.view(torch.int16).int() - want.view(torch.int16).int()).abs().max().item() <= 1
+    # the split plan: repeated calls take totals and counts from one allocation
+    xw = torch.randn(3, 5000, generator=g)
+    gw = 1 + 0.1 * torch.randn(5000, generator=g)
+    first = CG.run_rms_norm(xw.to(dev), gw.to(dev), eps=1e-6, plan="split")
+    for _ in range(3):
+        assert torch.equal(CG.run_rms_norm(xw.to(dev), gw.to(dev), eps=1e-6, plan="split"), first)
+    want = _from_raw(OX.rms_norm(_raw(xw), _raw(gw), "float32", 1e-6), torch.float32)
+    torch.testing.assert_close(first.cpu(), want, rtol=1e-5, atol=1e-6)
 
 
 def test_rms_cfg3_shape_and_strided_gamma():
