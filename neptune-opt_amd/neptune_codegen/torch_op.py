@@ -439,6 +439,28 @@ def _launch_segment(name, data, segments, params, plan, *, wrapper=None):
     Otherwise the spans are built and asserted exactly as `_segment_spans` does."""
     import torch
 
+    # CSR offsets seen before with the same tensor layout and parameters: the validation, the
+    # variant and the launch shape are what that call found; only the output allocation, the
+    # launch (span checks inside) and the assert on the armed status word remain
+    key = None
+    if (params["offsets"] and type(data) is torch.Tensor and type(segments) is torch.Tensor
+            and data.is_cuda and not hip.recording_active()):
+        try:
+            key = (name, plan, tuple(sorted((k, type(v).__name__, repr(v)) for k, v in params.items())),
+                   data.dtype, data.device, tuple(data.shape), tuple(data.stride()),
+                   data.data_ptr() % 16, segments.dtype, segments.device, tuple(segments.shape),
+                   tuple(segments.stride()))
+            entry = _SEG_SEEN.get(key)
+        except TypeError:
+            key, entry = None, None
+        status = _armed_status(data.device) if entry is not None else None
+        if status is not None:
+            out_shape, kernel, grid, tail = entry
+            out = torch.empty(out_shape, dtype=data.dtype, device=data.device)
+            kernel.launch(grid, (data.data_ptr(), segments.data_ptr(), out.data_ptr()) + tail,
+                          hip.current_stream(data.device))
+            torch._assert_async(status, DESCRIPTOR_MESSAGE)
+            return out
     shape = validate_segment_inputs(data, segments, reduce=name.removeprefix("segment_"),
                                     plan=plan, **params)
     channels = 1
@@ -458,15 +480,22 @@ def _launch_segment(name, data, segments, params, plan, *, wrapper=None):
             spans, _ = _device_spans(data, segments, offsets=params["offsets"])
         cover = -1 if params["offsets"] or params["unsafe"] else data.shape[0]
         flat = data.reshape(data.shape[0], channels)
-        launch_segment_kernel(compile_segment_reduction(name, params, plan), flat, spans, out,
-                              status=status, cover=cover)
+        launch = launch_segment_kernel(compile_segment_reduction(name, params, plan), flat, spans,
+                                       out, status=status, cover=cover)
         torch._assert_async(status, DESCRIPTOR_MESSAGE)
+        if (key is not None and flat.data_ptr() == data.data_ptr() and spans is segments
+                and status is _STATUS.get(data.device.index if data.device.index is not None
+                                          else torch.cuda.current_device())):
+            if len(_SEG_SEEN) >= 4096:
+                _SEG_SEEN.clear()
+            _SEG_SEEN[key] = (tuple(out.shape),) + launch
         return out
     _segment_spans(data, segments, offsets=params["offsets"], unsafe=params["unsafe"])
     return out
 
 
 _STATUS: dict = {}
+_SEG_SEEN: dict = {}
 
 
 def _armed_status(device):
@@ -504,10 +533,11 @@ def launch_segment_kernel(program, flat, spans, out, *, status=None, cover=-1):
         grid = (max(1, -(-nseg // (256 // var.lps))),)
     else:
         grid = (nseg, -(-channels // 64))
-    kernel.launch(grid, (flat.data_ptr(), spans.data_ptr(), out.data_ptr(), flat.shape[0],
-                         channels, nseg, flat.stride(0), flat.stride(1), spans.stride(0),
-                         status.data_ptr() if status is not None else 0, int(cover)),
+    tail = (flat.shape[0], channels, nseg, flat.stride(0), flat.stride(1), spans.stride(0),
+            status.data_ptr() if status is not None else 0, int(cover))
+    kernel.launch(grid, (flat.data_ptr(), spans.data_ptr(), out.data_ptr()) + tail,
                   hip.current_stream(flat.device))
+    return kernel, grid, tail
 
 
 def run_segment_pool(data, segments, *, reduce="sum", offsets=False, initial=None,

@@ -302,6 +302,29 @@ def test_l2_norm_whose_reciprocal_is_not_normal_takes_the_exact_division(dtype):
         assert torch.equal(got.view(view), want.view(view)), (got.view(view) != want.view(view)).nonzero()[:8].tolist()
 
 
+def test_repeated_segment_calls_reuse_their_launch_and_stay_exact():
+    """Repeated CSR-offset segment calls with the same layout reuse the first call's kernel and
+    launch shape; other offset values, another data alignment or another reduction must give
+    the C oracle's ordered results bit for bit."""
+    from oracle import exact as OX
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(25)
+    data = torch.randn(1001, 64, generator=g).bfloat16()
+    dd = data.to(dev)
+    for trial in range(3):
+        lengths = torch.randint(0, 40, (30,), generator=g)
+        offsets = torch.cat([torch.zeros(1, dtype=torch.int64), lengths.cumsum(0)])
+        offsets = offsets.clamp(max=1000)
+        for view, cpu in ((dd[:1000], data[:1000]), (dd[1:], data[1:])):
+            for reduce in ("sum", "mean", "sum"):
+                _say(f"segment repeated trial {trial} {reduce} offset {view.storage_offset()}")
+                got = CG.run_segment_pool(view, offsets.to(dev), reduce=reduce, offsets=True).cpu()
+                ref = _from_raw(OX.segment_pool(_raw(cpu.contiguous()), offsets.numpy(), "bfloat16",
+                                                mean=reduce == "mean", initial=None), torch.bfloat16)
+                assert torch.equal(torch.nan_to_num(got, 7.0), torch.nan_to_num(ref, 7.0)), (trial, reduce)
+
+
 def test_segment_fused_descriptor_check_matches_reference_asserts():
     """The span checks fused into the segment kernel clear the status word exactly when the
     reference's asserts (range, coverage unless unsafe, monotonic; torch_op.py:378-386, run here
