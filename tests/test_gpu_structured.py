@@ -323,6 +323,16 @@ def test_repeated_segment_calls_reuse_their_launch_and_stay_exact():
                 ref = _from_raw(OX.segment_pool(_raw(cpu.contiguous()), offsets.numpy(), "bfloat16",
                                                 mean=reduce == "mean", initial=None), torch.bfloat16)
                 assert torch.equal(torch.nan_to_num(got, 7.0), torch.nan_to_num(ref, 7.0)), (trial, reduce)
+    # int32 offsets and rank-3 data (channels flattened): other keys, same contract
+    data3 = torch.randn(600, 4, 16, generator=g).half()
+    for trial in range(2):
+        lengths = torch.randint(0, 30, (25,), generator=g)
+        off32 = torch.cat([torch.zeros(1, dtype=torch.int32), lengths.cumsum(0).to(torch.int32)]).clamp(max=600)
+        got = CG.run_segment_pool(data3.to(dev), off32.to(dev), reduce="sum", offsets=True).cpu()
+        ref = _from_raw(OX.segment_pool(_raw(data3.reshape(600, 64)), off32.numpy().astype("int64"),
+                                        "float16", mean=False, initial=None), torch.float16)
+        assert got.shape == (25, 4, 16)
+        assert torch.equal(got.reshape(25, 64), ref), trial
 
 
 def test_segment_fused_descriptor_check_matches_reference_asserts():
