@@ -306,7 +306,7 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* dst, in
 // score is the group sum of their partial dot products, and (m, l, O) are moved to every new
 // maximum exactly (not lazily).  Masked keys contribute nothing, so only the rows that see a
 // non-finite V value turn non-finite, as IEEE arithmetic on the visible keys gives.
-template <typename T, int D, bool CAUSAL, int W>
+template <typename T, int D, bool CAUSAL, int W, int BM = 32 * W>
 __device__ void attention_exact_rows(const T* __restrict__ qp, const T* __restrict__ kp,
                                      const T* __restrict__ vp, T* __restrict__ orow0,
                                      float* __restrict__ lse_row0, int sq, int sk, int q0,
@@ -315,7 +315,7 @@ __device__ void attention_exact_rows(const T* __restrict__ qp, const T* __restri
   constexpr int DQ = D / 4;                    // head dims per lane
   constexpr int ROWS = W * 64 / 4;             // queries per round
   const int tid = threadIdx.x, c = tid & 3;
-  for (int r0 = q0; r0 < q0 + 32 * W; r0 += ROWS) {
+  for (int r0 = q0; r0 < q0 + BM; r0 += ROWS) {
     const int my_q = r0 + (tid >> 2);
     const bool active = my_q < sq;
     float qv[DQ], ov[DQ];
@@ -609,26 +609,205 @@ __device__ __forceinline__ void attention_fwd(const T* __restrict__ q, const T* 
                                                    scale_log2);
     return;
   }
-  // ---- readout: O / l, and the natural-log LSE of the scaled scores
+  // ---- readout: O / l, and the natural-log LSE of the scaled scores.  The wave's 32 output
+  // rows go through its own 32 * D * 2 bytes of LDS (16-byte chunks XOR-swizzled by row) and
+  // out as whole rows, 16 bytes per lane; the barrier first lets every wave finish its reads
+  // of the last tile's buffers.
   const float l_lane = l_even + l_odd;
   const float l_tot = l_lane + partner<32>(l_lane);
   // l_tot is 0 only for a row whose visible scores are all -inf: 0 * inf = NaN, as softmax
   const float inv = 1.0f / l_tot;
-  if (my_q < sq) {
-    T* orow = orow0 + (i64)my_q * D;
+  __syncthreads();
+  // a tile buffer holds two waves' rows (TILE = 2 * 32 rows * D * 2 bytes)
+  constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  constexpr int SW = CPR < 16 ? CPR - 1 : 15;
+  unsigned char* const buf = wave < 2 ? kbuf0 : wave < 4 ? kbuf1 : wave < 6 ? vbuf0 : vbuf1;
+  unsigned char* stage = buf + (wave & 1) * (32 * D * 2);
 #pragma unroll
-    for (int a = 0; a < DBLK; ++a) {
+  for (int a = 0; a < DBLK; ++a) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u32x2 w;
-        w.x = In::pack2(oacc[a][4 * g + 0] * inv, oacc[a][4 * g + 1] * inv);
-        w.y = In::pack2(oacc[a][4 * g + 2] * inv, oacc[a][4 * g + 3] * inv);
-        *(u32x2*)(orow + a * 32 + 8 * g + 4 * hi) = w;
-      }
+    for (int g = 0; g < 4; ++g) {
+      u32x2 w;
+      w.x = In::pack2(oacc[a][4 * g + 0] * inv, oacc[a][4 * g + 1] * inv);
+      w.y = In::pack2(oacc[a][4 * g + 2] * inv, oacc[a][4 * g + 3] * inv);
+      *(u32x2*)(stage + l32 * (D * 2) + (((4 * a + g) ^ (l32 & SW)) << 4) + 8 * hi) = w;
     }
-    if (lse_row0 != nullptr && hi == 0)
-      lse_row0[my_q] = (m_ref + __builtin_log2f(l_tot)) * 0.6931471805599453f;
+  }
+  if (lse_row0 != nullptr && hi == 0 && my_q < sq)
+    lse_row0[my_q] = (m_ref + __builtin_log2f(l_tot)) * 0.6931471805599453f;
+  __builtin_amdgcn_wave_barrier();
+  if constexpr (CPR <= 64) {
+    constexpr int RPI = 64 / CPR;            // rows per wave-wide 16-byte-per-lane store
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int row = RPI * i + lane / CPR, c = lane % CPR;
+      const u32x4 w = *(const u32x4*)(stage + row * (D * 2) + ((c ^ (row & SW)) << 4));
+      if (qw + row < sq) store16(orow0 + (i64)(qw + row) * D + 8 * c, w);
+    }
   }
 }
+
+
+#ifdef NEP_ATTN_W64_ASM
+typedef u32 u32x8 __attribute__((ext_vector_type(8)));
+typedef u32 u32x32 __attribute__((ext_vector_type(32)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+
+// Head dim 128: one workgroup = 4 wave64s (one per SIMD) x 64 queries (two 32-query blocks per
+// wave) = 256 queries, so every K / V^T fragment read from LDS feeds two MFMAs.  The key-tile
+// loop is the instruction-scheduled block NEP_ATTN_W64_ASM (generated, with its register map,
+// by neptune_codegen/attention_asm.py): the softmax of tile t runs between the MFMAs of
+// S(t+1) = K(t+1) Q^T, the row sums of t and the row max of t+1 between those of
+// O^T += V^T(t) P^T(t).  Same arithmetic, operation for operation, as attention_fwd; same LDS
+// layouts (K rows of 16 swizzled chunks, the V^T image) in NBUF buffers each (the next NBUF-2
+// tiles in flight while t is computed), one barrier per tile.
+// This function prepares the per-lane addresses, pins them to the block's registers (the block
+// loads the Q^T operands itself, behind the first tile's DMA), and does the readout (or the
+// exact fp32 path) afterwards.  Q rows must be less than 2^22 elements apart.
+template <typename T, bool CAUSAL>
+__device__ __forceinline__ void attention_fwd_w64(const T* __restrict__ q, const T* __restrict__ k,
+                                                  const u16* __restrict__ vt,
+                                                  const int* __restrict__ exps,
+                                                  const T* __restrict__ v, T* __restrict__ o,
+                                                  float* __restrict__ lse, int heads, int sq,
+                                                  int sk, i64 qsb, i64 qsh, i64 qss, i64 ksb,
+                                                  i64 ksh, i64 kss, i64 vsb, i64 vsh, i64 vss,
+                                                  int e_max, float scale_log2) {
+  typedef AttnIn<T> In;
+  constexpr int D = 128, W = 4, BM = 256;
+  constexpr int TILE = kAttnBN * D * 2;
+  constexpr int NBUF = NEP_ATTN_W64_NBUF;   // K and V^T tile buffers
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * NBUF * TILE];   // K..., V...
+
+  const int nqb = (sq + BM - 1) / BM;
+  const int bh_count = gridDim.x / nqb;
+  const int id = blockIdx.x;
+  // Workgroups go to the XCDs round-robin (id % 8); each XCD takes its heads (head % 8 ==
+  // id % 8) two at a time, heaviest query block first within the pair, so the query blocks
+  // reading a head's K / V^T run together and share that XCD's L2.  Other head counts: the
+  // heaviest query block of every head first.
+  int qblk, bh;
+  if (bh_count % 8 == 0) {
+    const int x = id & 7, slot = id >> 3, hx_n = bh_count >> 3;
+    const int pair = slot / (2 * nqb), r = slot - pair * 2 * nqb;
+    int hx;
+    if (2 * pair + 1 < hx_n) {
+      qblk = nqb - 1 - (r >> 1);
+      hx = 2 * pair + (r & 1);
+    } else {
+      qblk = nqb - 1 - r;
+      hx = 2 * pair;
+    }
+    bh = hx * 8 + x;
+  } else {
+    qblk = nqb - 1 - id / bh_count;
+    bh = id % bh_count;
+  }
+  const int b = bh / heads, h = bh % heads;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int q0 = qblk * BM, qw = q0 + wave * 64;
+  const T* qp = q + b * qsb + h * qsh;
+  const T* kp = k + b * ksb + h * ksh;
+  const int ntiles_all = (sk + kAttnBN - 1) / kAttnBN;
+  const u16* vth = vt + (i64)bh * ntiles_all * (D * kAttnBN);
+  const int* eh = exps + bh * ntiles_all;
+
+  // Q rows of the workgroup: the loop loads its Q^T operands itself (rows past sq read 0)
+  const int qss2 = (int)(qss * 2);
+  const T* qbase = qp + (i64)q0 * qss;
+  const int q_nr = (min(sq - q0, BM) - 1) * qss2 + 256;
+  u32x2 qoff;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) qoff[blk] = (u32)((wave * 64 + 32 * blk + l32) * qss2 + 16 * hi);
+  int kv_end = sk;
+  if constexpr (CAUSAL) kv_end = min(sk, q0 + BM);
+  const int ntiles = (kv_end + kAttnBN - 1) / kAttnBN;
+  const int last_w = CAUSAL ? min(ntiles - 1, qw / kAttnBN) : ntiles - 1;
+  const u32 lds_base = lds_address(lds);
+  const int ksw = swizzle<16>(l32), vsw = swizzle<8>(l32);
+  u32x8 kaddr;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) kaddr[s] = lds_base + l32 * 256 + (((2 * s + hi) ^ ksw) << 4);
+  u32x4 vaddr;
+#pragma unroll
+  for (int cs = 0; cs < 4; ++cs)
+    vaddr[cs] = lds_base + NBUF * TILE + l32 * 128 + (((2 * cs + hi) ^ vsw) << 4);
+  // K DMA: 16 rows per round of the 4 waves; lane -> key 4*wave + lane/16, chunk lane%16
+  const int kss2 = (int)(kss * 2);
+  const int key = 4 * wave + (lane >> 4), part = lane & 15;
+  const int koff0 = key * kss2 + ((part ^ swizzle<16>(key)) << 4);
+  u32x4 koff;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) koff[i] = (u32)(koff0 + i * 16 * kss2);
+  u32x2 lb;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const int my_q = qw + 32 * blk + l32;
+    lb[blk] = (u32)((CAUSAL ? min(my_q, sk - 1) : sk - 1) - 4 * hi);
+  }
+  const u32 voff = lane * 16;
+
+  f32x32 oacc[4];
+  f32x8 st;   // m_ref[2], (l_even, l_odd)[2], tile max[2] (unused)
+  int exact;
+  asm volatile(NEP_ATTN_W64_ASM
+               : "={a[0:31]}"(oacc[0]), "={a[32:63]}"(oacc[1]), "={a[64:95]}"(oacc[2]),
+                 "={a[96:127]}"(oacc[3]), "={v[220:227]}"(st), "={s74}"(exact)
+               , "+{v[254:255]}"(qoff)
+               : "{s[98:99]}"(qbase), "{s97}"(q_nr), "{v[208:215]}"(kaddr),
+                 "{v[216:219]}"(vaddr), "{v[240:243]}"(koff), "{v[244:245]}"(lb), "{v246}"(voff),
+                 "{s[48:49]}"(kp), "{s[50:51]}"(vth), "{s[52:53]}"(eh), "{s54}"(kss2),
+                 "{s55}"(sk), "{s56}"(ntiles), "{s57}"(last_w), "{s58}"(scale_log2),
+                 "{s59}"(e_max), "{s60}"(qw), "{s61}"(lds_base), "{s63}"(wave)
+               : NEP_ATTN_W64_CLOBBERS);
+
+  T* orow0 = o + (i64)bh * sq * D;
+  float* lse_row0 = lse != nullptr ? lse + (i64)bh * sq : nullptr;
+  if (exact) {
+    attention_exact_rows<T, D, CAUSAL, W, BM>(qp, kp, v + b * vsb + h * vsh, orow0, lse_row0,
+                                             sq, sk, q0, qss, kss, vss, scale_log2);
+    return;
+  }
+  // ---- readout: O / l, and the natural-log LSE of the scaled scores.  The wave's 64 output
+  // rows go through its own 16 KB of LDS (16-byte chunks XOR-swizzled by row, conflict-free;
+  // every read of the loop is done: the loop ended with a barrier after its last reads), then
+  // out as whole rows, 16 bytes per lane.
+  unsigned char* stage = lds + wave * (64 * D * 2);
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const float l_lane = st[2 + 2 * blk] + st[3 + 2 * blk];
+    const float l_tot = l_lane + partner<32>(l_lane);
+    // l_tot is 0 only for a row whose visible scores are all -inf: 0 * inf = NaN, as softmax
+    const float inv = 1.0f / l_tot;
+    const int row = 32 * blk + l32;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = (a & 1) * 16 + 4 * g;
+        const f32x32& acc = oacc[blk * 2 + (a >> 1)];
+        u32x2 w;
+        w.x = In::pack2(acc[r + 0] * inv, acc[r + 1] * inv);
+        w.y = In::pack2(acc[r + 2] * inv, acc[r + 3] * inv);
+        *(u32x2*)(stage + row * (D * 2) + (((4 * a + g) ^ (row & 15)) << 4) + 8 * hi) = w;
+      }
+    }
+    const int my_q = qw + row;
+    if (lse_row0 != nullptr && hi == 0 && my_q < sq)
+      lse_row0[my_q] = (st[blk] + __builtin_log2f(l_tot)) * 0.6931471805599453f;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the wave's own LDS writes
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = 4 * i + (lane >> 4), c = lane & 15;
+    const u32x4 w = *(const u32x4*)(stage + row * (D * 2) + ((c ^ (row & 15)) << 4));
+    if (qw + row < sq) store16(orow0 + (i64)(qw + row) * D + 8 * c, w);
+  }
+}
+#endif  // NEP_ATTN_W64_ASM
 
 }  // namespace nep

@@ -26,7 +26,8 @@ import threading
 from neptune_codegen import hip
 from neptune_codegen.emitters import (ATTN_HEAD_DIMS, BASE_OPTIONS, attention_block_m,
                                       attention_fold_threads, attention_kernel_name,
-                                      attention_pack_kernel_name, emit_attention_source)
+                                      attention_pack_kernel_name, attention_w64,
+                                      emit_attention_source)
 
 _PROGRAMS: dict = {}
 _OPS: dict = {}
@@ -35,21 +36,40 @@ LOG2E = 1.4426950408889634
 BLOCK_M = 256           # queries per fold workgroup up to head dim 128 (8 waves of 32)
 BLOCK_N = 64            # keys per tile (one V^T image per tile)
 K_ROW_STRIDE_MAX = 1 << 24   # K rows are addressed with 32-bit byte offsets within a tile
+Q_ROW_STRIDE_MAX = 1 << 22   # head dim 128: Q rows, with 32-bit byte offsets within 256 rows
 # V^T tiles are fp16 images of v * 2^-e, e the tile's exponent (0 below 2^15).  A tile value
 # below 2^(e - 14) keeps only an absolute precision of 2^(e - 25), which bounds the error it
 # adds to O; e <= 13 keeps that under 2^-12, a quarter of the bf16 absolute tolerance.  Blocks
 # of queries that see a larger tile, or inf/NaN in V, take the exact fp32 path.  (fp32
 # accumulation of O, |O acc| <= keys * 2^8 * 2^28, cannot overflow at this bound.)
 V_EXPONENT_MAX = 13
+# Head dim 128 has two fold kernels with bit-identical results: 8 waves x 32 queries
+# (compiler-scheduled) and 4 waves x 64 queries (the instruction-scheduled loop of
+# attention_asm.py).  The second is faster per key tile (one LDS fragment feeds two MFMAs, the
+# softmax issues between them) but has the larger fixed cost per workgroup and idles a SIMD
+# whenever one of its waves is past its causal diagonal.  Measured crossovers on MI355X (op
+# time, same process): non-causal from 512 keys (0.93-0.97x), causal from 8192 queries
+# (0.93-0.99x); below them the 32-query kernel is faster (up to 1.15x at causal 512-1024).
+W64_MIN_SK = 512
+W64_CAUSAL_MIN_SQ = 8192
 
 
-def _program(head_dim: int, causal: bool, dtype="bfloat16") -> hip.Program:
-    key = (head_dim, causal, str(dtype))
+def use_w64(head_dim: int, causal: bool, sq: int, sk: int) -> bool:
+    """Whether a fold of this shape runs the 64-queries-per-wave kernel."""
+    if head_dim != 128:
+        return False
+    return sq >= W64_CAUSAL_MIN_SQ if causal else sk >= W64_MIN_SK
+
+
+def _program(head_dim: int, causal: bool, dtype="bfloat16", w64: bool | None = None) -> hip.Program:
+    w64 = attention_w64(head_dim, w64)
+    key = (head_dim, causal, str(dtype), w64)
     with _lock:
         prog = _PROGRAMS.get(key)
         if prog is None:
-            prog = hip.Program(emit_attention_source(head_dim, causal, dtype),
-                               f"{attention_kernel_name(head_dim, causal, dtype)}.hip", BASE_OPTIONS)
+            tag = "_w64" if w64 else ""
+            prog = hip.Program(emit_attention_source(head_dim, causal, dtype, w64=w64),
+                               f"{attention_kernel_name(head_dim, causal, dtype)}{tag}.hip", BASE_OPTIONS)
             _PROGRAMS[key] = prog
         return prog
 
@@ -99,9 +119,11 @@ def launch_attention(q, k, v, *, scale: float | None = None, causal: bool = True
     return _launch(q, k, v, scale, causal, return_lse, V_EXPONENT_MAX)
 
 
-def _launch(q, k, v, scale, causal, return_lse, e_max: int):
+def _launch(q, k, v, scale, causal, return_lse, e_max: int, w64: bool | None = None):
     """The launches with the exact path's threshold as a parameter: e_max = -1 sends every
-    query block through the exact fp32 path (the tests compare the two paths with it)."""
+    query block through the exact fp32 path (the tests compare the two paths with it).
+    `w64=False` runs the compiler-scheduled 32-queries-per-wave kernel at head dim 128 instead
+    of the instruction-scheduled one (the tests compare the two bit for bit)."""
     import torch
     from torch._subclasses.fake_tensor import FakeTensor
 
@@ -115,26 +137,31 @@ def _launch(q, k, v, scale, causal, return_lse, e_max: int):
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     if not math.isfinite(scale) or scale <= 0:
         raise ValueError("attention scale must be finite and positive")
+    if w64 is None:
+        w64 = use_w64(D, causal, Sq, k.shape[2])
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     if k.stride(2) >= K_ROW_STRIDE_MAX:
         k = k.contiguous()
+    if q.stride(2) >= Q_ROW_STRIDE_MAX:
+        q = q.contiguous()
     device = q.device.index if q.device.index is not None else torch.cuda.current_device()
     Sk = k.shape[2]
     ntiles = (Sk + BLOCK_N - 1) // BLOCK_N
     # V^T tile images (fp16, MFMA operand order) and one power-of-two exponent per tile
     vt = torch.empty((B * H * ntiles * D * BLOCK_N,), dtype=torch.float16, device=q.device)
     exps = torch.empty((B * H * ntiles,), dtype=torch.int32, device=q.device)
-    prog = _program(D, causal, q.dtype)
+    prog = _program(D, causal, q.dtype, w64)
     pack = prog.kernel(attention_pack_kernel_name(D, q.dtype),
                        (hip.PTR,) * 3 + (hip.I32,) * 2 + (hip.I64,) * 3, 256, device)
     fold = prog.kernel(attention_kernel_name(D, causal, q.dtype),
                        (hip.PTR,) * 7 + (hip.I32,) * 3 + (hip.I64,) * 9 + (hip.I32, hip.F32),
-                       attention_fold_threads(D), device)
+                       attention_fold_threads(D, w64), device)
     stream = hip.current_stream(q.device)
     pack.launch((B * H * ntiles,),
                 (v.data_ptr(), vt.data_ptr(), exps.data_ptr(), H, Sk,
                  v.stride(0), v.stride(1), v.stride(2)), stream)
-    nqb = (Sq + attention_block_m(D) - 1) // attention_block_m(D)
+    bm = attention_block_m(D, w64)
+    nqb = (Sq + bm - 1) // bm
     fold.launch((nqb * B * H,),
                 (q.data_ptr(), k.data_ptr(), vt.data_ptr(), exps.data_ptr(), v.data_ptr(),
                  out.data_ptr(), lse.data_ptr() if lse is not None else 0, H, Sq, Sk,

@@ -527,23 +527,32 @@ def segment_kernel_name(name: str, var: SegmentVariant) -> str:
 
 
 # ---------------------------------------------------------------- attention fold
-# The attention fold's workgroup: 8 wave64s (two per SIMD, <= 256 VGPRs each) up to head dim
-# 128, 4 (one per SIMD) at head dim 256; one workgroup per CU either way.
+# The attention fold's workgroup, one per CU: at head dim 64, 8 wave64s x 32 queries (two waves
+# per SIMD, <= 256 VGPRs each); at head dim 128, 4 wave64s x 64 queries (one wave per SIMD,
+# the instruction-scheduled loop of attention_asm.py); at head dim 256, 4 wave64s x 32 queries.
 ATTN_HEAD_DIMS = (64, 128, 256)
 
 
-def attention_waves(head_dim: int) -> int:
+def attention_w64(head_dim: int, w64: bool | None = None) -> bool:
+    """Whether the fold at this head dim is the 64-queries-per-wave kernel (head dim 128;
+    `w64=False` selects the compiler-scheduled 32-queries-per-wave kernel there instead)."""
+    return head_dim == 128 if w64 is None else (w64 and head_dim == 128)
+
+
+def attention_waves(head_dim: int, w64: bool | None = None) -> int:
+    if attention_w64(head_dim, w64):
+        return 4
     return 8 if head_dim <= 128 else 4
 
 
-def attention_fold_threads(head_dim: int) -> int:
-    return 64 * attention_waves(head_dim)
+def attention_fold_threads(head_dim: int, w64: bool | None = None) -> int:
+    return 64 * attention_waves(head_dim, w64)
 
 
-def attention_block_m(head_dim: int) -> int:
-    """Queries per fold workgroup (32 per wave)."""
-    return 32 * attention_waves(head_dim)
-
+def attention_block_m(head_dim: int, w64: bool | None = None) -> int:
+    """Queries per fold workgroup."""
+    per_wave = 64 if attention_w64(head_dim, w64) else 32
+    return per_wave * attention_waves(head_dim, w64)
 
 
 ATTN_DTYPES = {"bfloat16": ("bf16", "__bf16"), "float16": ("f16", "_Float16")}
@@ -557,22 +566,31 @@ def _attn_dtype(dtype) -> tuple[str, str]:
 
 
 def emit_attention_source(head_dim: int, causal: bool, dtype="bfloat16",
-                          waves_per_eu: int | None = None) -> str:
+                          waves_per_eu: int | None = None, w64: bool | None = None) -> str:
     """hiprtc unit of the online-softmax attention fold (no reference counterpart): the
     logsumexp repair exp(s - s2) applied per key tile to (m, l, O).  Holds two kernels: the
     V^T tile packer and the fold itself (with its exact fallback for out-of-range V)."""
     if head_dim not in ATTN_HEAD_DIMS:
         raise NotImplementedError("attention fold supports head_dim 64, 128 and 256")
-    wpe = attention_waves(head_dim) // 4 if waves_per_eu is None else waves_per_eu
-    threads = attention_fold_threads(head_dim)
+    w64 = attention_w64(head_dim, w64)
+    wpe = attention_waves(head_dim, w64) // 4 if waves_per_eu is None else waves_per_eu
+    threads = attention_fold_threads(head_dim, w64)
     tag, ctype = _attn_dtype(dtype)
     name = attention_kernel_name(head_dim, causal, dtype)
     pack = attention_pack_kernel_name(head_dim, dtype)
+    cz = "true" if causal else "false"
+    if w64:
+        from neptune_codegen.attention_asm import asm_macro
+        prefix = asm_macro(causal, tag) + "\n"
+        call = f"  nep::attention_fwd_w64<{ctype}, {cz}>("
+    else:
+        prefix = ""
+        call = f"  nep::attention_fwd<{ctype}, {head_dim}, {cz}>("
     return "\n".join([
         "// AUTO-GENERATED by neptune_codegen (HIP emitter) -- do not edit.\n"
         f"// online-softmax attention fold: head_dim={head_dim}, causal={causal}, {tag} inputs; "
         f"{tag} MFMA for Q K^T, fp16 MFMA for P V, fp32 running max/sum.\n",
-        kernel_header("nep_device.h", "nep_attention.h"),
+        prefix + kernel_header("nep_device.h", "nep_attention.h"),
         f'extern "C" __global__ void __launch_bounds__(256) {pack}(const void* v, void* vt, int* exps, '
         "int heads, int sk, long long vsb, long long vsh, long long vss) {\n"
         f"  nep::attention_vt_pack<{ctype}, {head_dim}>((const {ctype}*)v, (nep::u16*)vt, exps, "
@@ -581,7 +599,7 @@ def emit_attention_source(head_dim: int, causal: bool, dtype="bfloat16",
         "const void* vt, const int* exps, const void* v, void* o, float* lse, int heads, int sq, "
         "int sk, long long qsb, long long qsh, long long qss, long long ksb, long long ksh, "
         "long long kss, long long vsb, long long vsh, long long vss, int e_max, float scale_log2) {\n"
-        f"  nep::attention_fwd<{ctype}, {head_dim}, {'true' if causal else 'false'}>((const {ctype}*)q, "
+        + call + f"(const {ctype}*)q, "
         f"(const {ctype}*)k, (const nep::u16*)vt, exps, (const {ctype}*)v, ({ctype}*)o, lse, heads, "
         "sq, sk, qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss, e_max, scale_log2);\n}\n"])
 
