@@ -133,7 +133,7 @@ def test_emitted_units_compile_for_gfx950():
         assert hip.compile_code_object(src, "seg.hip", E.BASE_OPTIONS + E.NO_CONTRACT, write_cache=False) > 0
     for w64 in (True, False):      # head dim 128: both fold kernels
         src = E.emit_attention_source(128, True, w64=w64)
-        assert ("NEP_ATTN_W64_ASM" in src) == w64
+        assert ("#define NEP_ATTN_W64_ASM" in src) == w64
         assert hip.compile_code_object(src, "attn.hip", E.BASE_OPTIONS, write_cache=False) > 0
     assert len(set(names)) == len(names)
 
