@@ -575,30 +575,33 @@ __device__ __forceinline__ void attention_fwd(const T* __restrict__ q, const T* 
   // Tile t is computed from buffers t % 2 while the DMA of tile t+1 fills the others (last
   // read in iteration t-1, before this iteration's barrier).  Unrolled by two so every LDS
   // address names its array.
-  // The exponent of tile t+1 is loaded at the top of iteration t, ahead of that iteration's
-  // DMA: vmcnt retires in order, so a later wait on it would also wait for the DMA.  Every
-  // wave reads every exponent of the block's key range, so `exact` is workgroup-uniform.
+  // Every wave reads every exponent of the block's key range, so `exact` is workgroup-uniform.
   bool exact = false;
+  // e_pending (per lane, the same in all) is loaded one iteration ahead and made uniform only
+  // after the next wait_dma, which retires it with the DMA: the load's latency is never waited
+  // for on its own.
+  int e_pending = ntiles > 0 ? eh[0] : 0;
   if (ntiles > 0) issue(0, kbuf0, vbuf0);
-  int e_cur = ntiles > 0 ? eh[0] : 0;
   for (int tile = 0; tile < ntiles;) {
     wait_dma();
     __syncthreads();
-    int e_next = tile + 1 < ntiles ? eh[tile + 1] : 0;
+    asm volatile("" : "+v"(e_pending));
+    int e_cur = __builtin_amdgcn_readfirstlane(e_pending);
+    e_pending = tile + 1 < ntiles ? eh[tile + 1] : 0;
     __builtin_amdgcn_sched_barrier(0);
     if (tile + 1 < ntiles) issue(tile + 1, kbuf1, vbuf1);
     exact |= e_cur > e_max;
     body(tile, kbuf0, vbuf0, e_cur);
-    e_cur = e_next;
     if (++tile >= ntiles) break;
     wait_dma();
     __syncthreads();
-    e_next = tile + 1 < ntiles ? eh[tile + 1] : 0;
+    asm volatile("" : "+v"(e_pending));
+    e_cur = __builtin_amdgcn_readfirstlane(e_pending);
+    e_pending = tile + 1 < ntiles ? eh[tile + 1] : 0;
     __builtin_amdgcn_sched_barrier(0);
     if (tile + 1 < ntiles) issue(tile + 1, kbuf0, vbuf0);
     exact |= e_cur > e_max;
     body(tile, kbuf1, vbuf1, e_cur);
-    e_cur = e_next;
     ++tile;
   }
   T* orow0 = o + (i64)bh * sq * D;
