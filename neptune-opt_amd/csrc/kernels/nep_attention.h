@@ -199,7 +199,7 @@ __device__ __forceinline__ void attention_vt_pack(const T* __restrict__ v, u16* 
 #pragma unroll
   for (int c = tid; c < D * kAttnBN / 8; c += kAttnThreads)
     store16(dst + c * 8, *(const u32x4*)(img + c * 8));
-  if (tid == 0) exps[bh * ntiles + t] = bad ? kVtNonFinite : e_tile;
+  if (tid == 0) exps[(i64)bh * ntiles + t] = bad ? kVtNonFinite : e_tile;
 }
 
 // 32-bit LDS address of a pointer into __shared__ memory.
@@ -432,7 +432,7 @@ __device__ __forceinline__ void attention_fwd(const T* __restrict__ q, const T* 
   const T* kp = k + b * ksb + h * ksh;
   const int ntiles_all = (sk + kAttnBN - 1) / kAttnBN;
   const u16* vth = vt + (i64)bh * ntiles_all * (D * kAttnBN);
-  const int* eh = exps + bh * ntiles_all;
+  const int* eh = exps + (i64)bh * ntiles_all;
 
   // Q^T operand: query my_q, head dims [16s + 8*hi, +8) for k-step s.
   vec8 qreg[KSTEPS];
@@ -716,7 +716,7 @@ __device__ __forceinline__ void attention_fwd_w64(const T* __restrict__ q, const
   const T* kp = k + b * ksb + h * ksh;
   const int ntiles_all = (sk + kAttnBN - 1) / kAttnBN;
   const u16* vth = vt + (i64)bh * ntiles_all * (D * kAttnBN);
-  const int* eh = exps + bh * ntiles_all;
+  const int* eh = exps + (i64)bh * ntiles_all;
 
   // Q rows of the workgroup: the loop loads its Q^T operands itself (rows past sq read 0)
   const int qss2 = (int)(qss * 2);
