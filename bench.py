@@ -262,6 +262,9 @@ def per_fold(dev, xs_cpu, xs_dev, cpu: bool = True):
     ms = graph_time(lambda i: CG.run_attention(q, k, v, causal=True), replays=3, inner=4)
     flops = 4 * 4 * 32 * 128 * 4096 * 4097 // 2
     tflops = flops / (ms * 1e-3) / 1e12
+    # the same shape without the mask: the head-dim-128 fold's 64-queries-per-wave kernel
+    ms_full = graph_time(lambda i: CG.run_attention(q, k, v, causal=False), replays=3, inner=2)
+    flops_full = 4 * 4 * 32 * 128 * 4096 * 4096
     del q, k, v
     gemm = gemm_ceiling_tflops(dev)
     key5 = "cfg5_attention_causal_bf16_4x32x4096x128"
@@ -271,6 +274,11 @@ def per_fold(dev, xs_cpu, xs_dev, cpu: bool = True):
         "bf16_gemm_TFLOP_s": round(gemm, 1), "frac_of_bf16_gemm": round(tflops / gemm, 4),
         "rocprof_pmc": attention_pmc()}
     log(f"[bench] cfg5 attention: {folds[key5]}")
+    folds["attention_full_bf16_4x32x4096x128"] = {
+        "us": round(ms_full * 1e3, 1), "TFLOP_s": round(flops_full / (ms_full * 1e-3) / 1e12, 1),
+        "frac_of_bf16_gemm": round(flops_full / (ms_full * 1e-3) / 1e12 / gemm, 4),
+        "kernel": "64 queries per wave (attention.use_w64)"}
+    log(f"[bench] attention without the mask: {folds['attention_full_bf16_4x32x4096x128']}")
     folds["reference_shapes"] = reference_shapes(dev)
     qh, kh, vh = (t[0:1, 0:2] for t in qkv)
     beside(key5, "cfg5 attention", lambda: R.attention_reference(qh, kh, vh, causal=True),
