@@ -74,9 +74,11 @@ def _segment_programs():
 def _attention_programs():
     from neptune_codegen.attention import _program
 
-    return [_program(128, True), _program(128, False), _program(64, True), _program(64, False),
-            _program(128, True, "float16"), _program(64, False, "float16"), _program(256, True),
-            _program(256, False), _program(256, True, "float16")]
+    # head dim 128: both fold kernels (attention.use_w64 picks one by shape)
+    return [_program(128, c, dt, w) for c in (True, False) for dt in ("bfloat16", "float16")
+            for w in (True, False)] + [
+        _program(64, True), _program(64, False), _program(64, False, "float16"),
+        _program(256, True), _program(256, False), _program(256, True, "float16")]
 
 
 def programs():
