@@ -67,9 +67,8 @@ def _program(head_dim: int, causal: bool, dtype="bfloat16", w64: bool | None = N
     with _lock:
         prog = _PROGRAMS.get(key)
         if prog is None:
-            tag = "_w64" if w64 else ""
             prog = hip.Program(emit_attention_source(head_dim, causal, dtype, w64=w64),
-                               f"{attention_kernel_name(head_dim, causal, dtype)}{tag}.hip", BASE_OPTIONS)
+                               f"{attention_kernel_name(head_dim, causal, dtype, w64)}.hip", BASE_OPTIONS)
             _PROGRAMS[key] = prog
         return prog
 
@@ -153,7 +152,7 @@ def _launch(q, k, v, scale, causal, return_lse, e_max: int, w64: bool | None = N
     prog = _program(D, causal, q.dtype, w64)
     pack = prog.kernel(attention_pack_kernel_name(D, q.dtype),
                        (hip.PTR,) * 3 + (hip.I32,) * 2 + (hip.I64,) * 3, 256, device)
-    fold = prog.kernel(attention_kernel_name(D, causal, q.dtype),
+    fold = prog.kernel(attention_kernel_name(D, causal, q.dtype, attention_w64(D, w64)),
                        (hip.PTR,) * 7 + (hip.I32,) * 3 + (hip.I64,) * 9 + (hip.I32, hip.F32),
                        attention_fold_threads(D, w64), device)
     stream = hip.current_stream(q.device)

@@ -576,7 +576,7 @@ def emit_attention_source(head_dim: int, causal: bool, dtype="bfloat16",
     wpe = attention_waves(head_dim, w64) // 4 if waves_per_eu is None else waves_per_eu
     threads = attention_fold_threads(head_dim, w64)
     tag, ctype = _attn_dtype(dtype)
-    name = attention_kernel_name(head_dim, causal, dtype)
+    name = attention_kernel_name(head_dim, causal, dtype, w64)
     pack = attention_pack_kernel_name(head_dim, dtype)
     cz = "true" if causal else "false"
     if w64:
@@ -604,9 +604,11 @@ def emit_attention_source(head_dim: int, causal: bool, dtype="bfloat16",
         "sq, sk, qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss, e_max, scale_log2);\n}\n"])
 
 
-def attention_kernel_name(head_dim: int, causal: bool, dtype="bfloat16") -> str:
+def attention_kernel_name(head_dim: int, causal: bool, dtype="bfloat16", w64: bool = False) -> str:
+    """The fold's symbol; the 64-queries-per-wave kernel carries a `_w64` suffix."""
     tag, _ = _attn_dtype(dtype)
-    return f"attention_fold_{tag}_d{head_dim}_{'causal' if causal else 'full'}"
+    suffix = "_w64" if attention_w64(head_dim, w64) and w64 else ""
+    return f"attention_fold_{tag}_d{head_dim}_{'causal' if causal else 'full'}{suffix}"
 
 
 def attention_pack_kernel_name(head_dim: int, dtype="bfloat16") -> str:
