@@ -693,9 +693,11 @@ def main():
     ap.add_argument("--compile-best", action="store_true",
                     help="only run neptune_opt.compile_best (AOTI baseline vs fused package, "
                          "verified and A/B timed) on models built around the configs, then exit")
-    ap.add_argument("--attention-probe", action="store_true",
-                    help="only run the cfg5 attention fold (5 calls), for rocprofv3 --pmc runs "
-                         "(MFMA busy cycles, clock)")
+    ap.add_argument("--attention-probe", nargs="?", const="causal", default=None,
+                    choices=("causal", "full"),
+                    help="only run the cfg5 attention fold (5 calls; 'full': the same shape "
+                         "without the mask, the 64-queries-per-wave kernel), for rocprofv3 "
+                         "--pmc runs (MFMA busy cycles, clock)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; every fold is row/segment-parallel and "
@@ -744,7 +746,7 @@ def main():
         g5 = seeded(5)
         q, k, v = ((torch.randn(4, 32, 4096, 128, generator=g5).bfloat16()).to(dev) for _ in range(3))
         for _ in range(5):
-            CG.run_attention(q, k, v, causal=True)
+            CG.run_attention(q, k, v, causal=args.attention_probe == "causal")
         torch.cuda.synchronize()
         log("[bench] attention probe done")
         return
