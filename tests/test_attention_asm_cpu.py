@@ -153,6 +153,37 @@ def test_wait_states_along_execution_paths(causal, op, policy):
     assert checked > (0 if policy == "idle wave" else 100)
 
 
+def _check_lds_waits(trace):
+    """Simulate lgkmcnt: LDS reads retire in order; s_waitcnt lgkmcnt(n) leaves the n newest
+    outstanding (a scalar load in flight only makes a wait stricter, so it is not counted).
+    No MFMA may read a register an outstanding read is still filling."""
+    pending = []          # registers per outstanding LDS read, oldest first
+    checked = 0
+    for line in trace:
+        op, _, rest = line.partition(" ")
+        if op.startswith("ds_read"):
+            pending.append(set(_regs(rest.split(",")[0])))
+        elif op == "s_waitcnt" and "lgkmcnt" in rest:
+            n = int(re.search(r"lgkmcnt\((\d+)\)", rest).group(1))
+            pending = pending[len(pending) - n:] if n < len(pending) else pending
+        elif op.startswith("v_mfma"):
+            srcs = set()
+            for part in [p.strip() for p in rest.split(",")][1:3]:
+                srcs |= set(_regs(part))
+            for regs in pending:
+                assert not (regs & srcs), line
+            checked += 1
+    return checked
+
+
+@pytest.mark.parametrize("policy", sorted(POLICIES))
+@pytest.mark.parametrize("causal,op", VARIANTS)
+def test_mfma_operands_wait_for_their_lds_reads(causal, op, policy):
+    lines = X.generate_loop(causal, op).splitlines()
+    trace = _walk(lines, POLICIES[policy])
+    assert _check_lds_waits(trace) > (10 if policy == "idle wave" else 200)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_tile_work_counts(causal):
     text = X.generate_loop(causal, "bf16")
