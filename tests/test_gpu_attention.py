@@ -287,6 +287,26 @@ def test_attention_rows_whose_scores_are_all_minus_inf(causal, exact):
     torch.testing.assert_close(lse[keep], _lse_reference(q, k, causal)[keep], rtol=LSE_RTOL, atol=LSE_ATOL)
 
 
+@pytest.mark.parametrize("D,sq,sk,causal", [(64, 200, 90001, False), (256, 130, 70001, False),
+                                             (64, 4500, 4500, True), (256, 2100, 2100, True)])
+def test_attention_long_key_ranges_other_head_dims(D, sq, sk, causal):
+    """Head dims 64 and 256 over more than a thousand key tiles (ragged last tile) and over
+    long causal folds, against the fp32 closed form computed on the GPU."""
+    dev = _dev()
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(1, 1, sq, D, generator=g).bfloat16().to(dev)
+    k, v = (torch.randn(1, 1, sk, D, generator=g).bfloat16().to(dev) for _ in range(2))
+    _say(f"attention long keys D={D} Sq={sq} Sk={sk} causal={causal}")
+    got, lse = CG.run_attention(q, k, v, causal=causal, return_lse=True)
+    s = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) / math.sqrt(D)
+    if causal:
+        s = s.masked_fill(~torch.ones(sq, sk, dtype=torch.bool, device=dev).tril(0),
+                          float("-inf"))
+    want = torch.matmul(torch.softmax(s, -1), v.float())
+    torch.testing.assert_close(got.float(), want, rtol=1.6e-2, atol=1e-3)
+    torch.testing.assert_close(lse, torch.logsumexp(s, -1), rtol=LSE_RTOL, atol=LSE_ATOL)
+
+
 def test_attention_strided_layout_and_scale():
     """[B, S, H, D] storage viewed as [B, H, S, D] (the common projection layout)."""
     dev = _dev()
