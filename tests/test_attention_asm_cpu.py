@@ -11,6 +11,10 @@ emitted text with checkers written independently of the generator's own bookkeep
     state, s_nop n is n + 1);
   * every MFMA reading a fragment quad waits (s_waitcnt lgkmcnt) for the LDS read that filled
     it, LDS reads retiring in order;
+  * the DMA pipeline (vmcnt and barriers simulated): an LDS K / V^T buffer is read only after
+    its DMA has landed in every wave and a barrier followed, a DMA overwrites a buffer only
+    after a barrier that every wave reached with its reads of it retired, and no MFMA reads a
+    Q^T register a buffer load is still filling;
   * per tile and wave: 64 MFMAs, 32 fragment reads, 64 exponentials;
   * the selection rule between the two kernels.
 """
@@ -182,6 +186,79 @@ def test_mfma_operands_wait_for_their_lds_reads(causal, op, policy):
     lines = X.generate_loop(causal, op).splitlines()
     trace = _walk(lines, POLICIES[policy])
     assert _check_lds_waits(trace) > (10 if policy == "idle wave" else 200)
+
+
+def _lds_region(line):
+    """(operand, buffer) an LDS fragment read addresses: K through v208-v215, V^T through
+    v216-v219, 16 KB per buffer."""
+    m = re.search(r", v(\d+)(?: offset:(\d+))?$", line)
+    reg, off = int(m.group(1)), int(m.group(2) or 0)
+    return ("K" if reg < X.VADDR else "V", off // 16384)
+
+
+def _check_dma_pipeline(trace):
+    """Simulate vmcnt (vector loads retire in order), lgkmcnt and barriers for one wave; every
+    wave runs the same checks, so a condition that holds here at a barrier holds in all."""
+    vm = []                   # outstanding vector loads: ("lds", region) or ("reg", registers)
+    lgkm = []                 # outstanding LDS reads: region
+    pending, state = {}, {}   # region -> DMA pieces in flight; "landed" / "visible"
+    read_since_barrier = set()
+    m0 = None
+    reads = 0
+    for line in trace:
+        op, _, rest = line.partition(" ")
+        if op == "s_add_i32" and rest.startswith("m0,"):
+            _, base, off = [p.strip() for p in rest.split(",")]
+            m0 = ("K" if base == "s90" else "V", int(off) // 16384)
+        elif op.startswith("buffer_load"):
+            if rest.endswith(" lds"):
+                assert m0 not in read_since_barrier and m0 not in lgkm, line
+                pending[m0] = pending.get(m0, 0) + 1
+                state[m0] = "pending"
+                vm.append(("lds", m0))
+            else:
+                vm.append(("reg", set(_regs(rest.split(",")[0]))))
+        elif op == "s_waitcnt":
+            n = re.search(r"vmcnt\((\d+)\)", rest)
+            if n:
+                keep = int(n.group(1))
+                done, vm = (vm[:len(vm) - keep], vm[len(vm) - keep:]) if keep < len(vm) else ([], vm)
+                for kind, what in done:
+                    if kind == "lds":
+                        pending[what] -= 1
+                        if pending[what] == 0:
+                            state[what] = "landed"
+            n = re.search(r"lgkmcnt\((\d+)\)", rest)
+            if n:
+                keep = int(n.group(1))
+                lgkm = lgkm[len(lgkm) - keep:] if keep < len(lgkm) else lgkm
+        elif op == "s_barrier":
+            assert not lgkm, "barrier with LDS reads in flight"
+            for region, st in state.items():
+                if st == "landed":
+                    state[region] = "visible"
+            read_since_barrier.clear()
+        elif op.startswith("ds_read"):
+            region = _lds_region(line)
+            assert state.get(region) == "visible", line
+            read_since_barrier.add(region)
+            lgkm.append(region)
+            reads += 1
+        elif op.startswith("v_mfma"):
+            srcs = set()
+            for part in [p.strip() for p in rest.split(",")][1:3]:
+                srcs |= set(_regs(part))
+            for kind, what in vm:
+                assert kind != "reg" or not (what & srcs), line
+    return reads
+
+
+@pytest.mark.parametrize("policy", sorted(POLICIES))
+@pytest.mark.parametrize("causal,op", VARIANTS)
+def test_dma_pipeline_buffers(causal, op, policy):
+    lines = X.generate_loop(causal, op).splitlines()
+    trace = _walk(lines, POLICIES[policy])
+    assert _check_dma_pipeline(trace) >= 16
 
 
 @pytest.mark.parametrize("causal", [True, False])
