@@ -261,6 +261,30 @@ def test_dma_pipeline_buffers(causal, op, policy):
     assert _check_dma_pipeline(trace) >= 16
 
 
+def _s_tile_macro_lines():
+    """Instructions of the 32-query kernel's S-phase asm block (NEP_ATTN_S_TILE_D128)."""
+    import pathlib
+
+    text = (pathlib.Path(X.__file__).parents[1] / "csrc" / "kernels" / "nep_attention.h").read_text()
+    start = text.index("#define NEP_ATTN_S_TILE_D128(OP)")
+    body = text[start:text.index(": [s0]", start)]
+    return [l.replace('" OP "', "bf16") for l in re.findall(r'"((?:[^"\\]|" OP ")*)\\n"', body)]
+
+
+def test_s_tile_block_of_the_32_query_kernel():
+    """Its K fragments: 16 reads into eight quads, each MFMA waits for its own read (lgkmcnt),
+    each quad refilled at least 2 wait states after the MFMA that read it, and 20 wait states
+    after the last MFMA before the compiler's code may read the scores."""
+    lines = _s_tile_macro_lines()
+    assert sum(l.startswith("ds_read_b128") for l in lines) == 16
+    assert sum(l.startswith("v_mfma") for l in lines) == 16
+    assert _check_lds_waits(lines) == 16
+    _check_hazards(lines)
+    last = max(i for i, l in enumerate(lines) if l.startswith("v_mfma"))
+    tail = sum(int(l.split()[1]) + 1 if l.startswith("s_nop") else 1 for l in lines[last + 1:])
+    assert tail >= X.W_MFMA_VALU
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_tile_work_counts(causal):
     text = X.generate_loop(causal, "bf16")
