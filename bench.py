@@ -262,7 +262,7 @@ def per_fold(dev, xs_cpu, xs_dev, cpu: bool = True):
     ms = graph_time(lambda i: CG.run_attention(q, k, v, causal=True), replays=3, inner=4)
     flops = 4 * 4 * 32 * 128 * 4096 * 4097 // 2
     tflops = flops / (ms * 1e-3) / 1e12
-    # the same shape without the mask: the head-dim-128 fold's 64-queries-per-wave kernel
+    # the same shape without the mask
     ms_full = graph_time(lambda i: CG.run_attention(q, k, v, causal=False), replays=3, inner=2)
     flops_full = 4 * 4 * 32 * 128 * 4096 * 4096
     del q, k, v
@@ -272,12 +272,12 @@ def per_fold(dev, xs_cpu, xs_dev, cpu: bool = True):
         "us": round(ms * 1e3, 1), "TFLOP_s": round(tflops, 1), "frac_mfma_bf16": round(tflops / BF16_PEAK, 4),
         "flops": flops, "query_rows_per_s": round(4 * 32 * 4096 / (ms * 1e-3), 1),
         "bf16_gemm_TFLOP_s": round(gemm, 1), "frac_of_bf16_gemm": round(tflops / gemm, 4),
-        "rocprof_pmc": attention_pmc()}
+        "kernel": kernel_of(True), "rocprof_pmc": attention_pmc()}
     log(f"[bench] cfg5 attention: {folds[key5]}")
     folds["attention_full_bf16_4x32x4096x128"] = {
         "us": round(ms_full * 1e3, 1), "TFLOP_s": round(flops_full / (ms_full * 1e-3) / 1e12, 1),
         "frac_of_bf16_gemm": round(flops_full / (ms_full * 1e-3) / 1e12 / gemm, 4),
-        "kernel": "64 queries per wave (attention.use_w64)"}
+        "kernel": kernel_of(False)}
     log(f"[bench] attention without the mask: {folds['attention_full_bf16_4x32x4096x128']}")
     folds["reference_shapes"] = reference_shapes(dev)
     qh, kh, vh = (t[0:1, 0:2] for t in qkv)
@@ -657,10 +657,18 @@ def gemm_ceiling_tflops(dev, n: int = 8192, calls: int = 10) -> float:
     return 2 * n ** 3 / (ms * 1e-3) / 1e12
 
 
+def kernel_of(causal: bool) -> str:
+    """Which head-dim-128 fold kernel attention.use_w64 picks at the cfg5 shape."""
+    from neptune_codegen import attention as A
+
+    return ("64 queries per wave" if A.use_w64(128, causal, 4096, 4096) else
+            "32 queries per wave") + " (attention.use_w64)"
+
+
 def attention_pmc():
     """MFMA busy fraction and clock of the attention fold from the committed rocprofv3 PMC
     summary (SQ_VALU_MFMA_BUSY_CYCLES over active cycles x SIMDs), or None when absent."""
-    path = ROOT / "profiles" / "attention_causal_bf16_4x32x4096x128_pmc.md"
+    path = ROOT / "profiles" / "attention_causal_bf16_4x32x4096x128_w64_pmc.md"
     if not path.exists():
         return None
     out = {}
@@ -696,8 +704,7 @@ def main():
     ap.add_argument("--attention-probe", nargs="?", const="causal", default=None,
                     choices=("causal", "full"),
                     help="only run the cfg5 attention fold (5 calls; 'full': the same shape "
-                         "without the mask, the 64-queries-per-wave kernel), for rocprofv3 "
-                         "--pmc runs (MFMA busy cycles, clock)")
+                         "without the mask), for rocprofv3 --pmc runs (MFMA busy cycles, clock)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; every fold is row/segment-parallel and "

@@ -47,11 +47,12 @@ V_EXPONENT_MAX = 13
 # (compiler-scheduled) and 4 waves x 64 queries (the instruction-scheduled loop of
 # attention_asm.py).  The second is faster per key tile (one LDS fragment feeds two MFMAs, the
 # softmax issues between them) but has the larger fixed cost per workgroup and idles a SIMD
-# whenever one of its waves is past its causal diagonal.  Measured crossovers on MI355X (op
-# time, same process): non-causal from 512 keys (0.93-0.97x), causal from 8192 queries
-# (0.93-0.99x); below them the 32-query kernel is faster (up to 1.15x at causal 512-1024).
+# whenever one of its waves is past its causal diagonal.  Measured op-time ratios on MI355X
+# (graph replays, the two kernels interleaved in one process, two boxes): non-causal 0.93-0.97
+# from 512 keys (1.08 at 256); causal 0.957-0.990 from 3072 queries (B*H 32-128), 0.985 at
+# 2048 and 1.03 at 1024, 1536 and 2560.
 W64_MIN_SK = 512
-W64_CAUSAL_MIN_SQ = 8192
+W64_CAUSAL_MIN_SQ = 3072
 
 
 def use_w64(head_dim: int, causal: bool, sq: int, sk: int) -> bool:
