@@ -519,7 +519,10 @@ def mask_block(em: Emitter, xbuf: int, tile_sreg: str, causal: bool, tag: str):
 
 def rescale_block(em: Emitter, tag: str):
     """Lazy rescale check of tile t (tile max in TMAX) and, when a lane's max moved, the
-    rescale of (m_ref, l, O) for both query blocks."""
+    rescale of (m_ref, l, O) for both query blocks.  While every lane's m_ref is still -inf
+    (a wave's first tile with a finite score), the factor is 0 and l and O hold only zeros
+    (or NaN from 0 * inf/NaN in V), which multiplying by 0 leaves as they are: only m_ref
+    moves then."""
     lift = T0
     em.valu("v_cvt_f32_u32 v230, s76", (), (lift,))
     for qb in (0, 1):
@@ -530,6 +533,11 @@ def rescale_block(em: Emitter, tag: str):
     em.nop(4)
     em.salu("s_or_b64 s[88:89], s[80:81], s[82:83]")
     em.branch("s_cbranch_scc0", f"norescale{tag}")
+    em.valu(f"v_cmp_neq_f32 vcc, s86, v{MREF}", (MREF,), (), mask_out="vcc")
+    em.valu(f"v_cmp_neq_f32_e64 s[84:85], s86, v{MREF + 1}", (MREF + 1,), (), mask_out="s84")
+    em.nop(4)
+    em.salu("s_or_b64 s[84:85], vcc, s[84:85]")
+    em.branch("s_cbranch_scc0", f"firstrescale{tag}")
     for qb in (0, 1):
         tl, mr, pair = T0 + 1 + qb, MREF + qb, f"s[{80 + 2 * qb}:{81 + 2 * qb}]"
         mn, al = T0 + 5, T0 + 6
@@ -552,6 +560,12 @@ def rescale_block(em: Emitter, tag: str):
                 for i in range(8):
                     em.valu(f"v_accvgpr_write_b32 {_rname(base + g + i)}, v{tmp[i]}", (tmp[i],), (base + g + i,))
         em.valu(f"v_mov_b32 v{mr}, v{mn}", (mn,), (mr,))
+    em.branch("s_branch", f"norescale{tag}")
+    em.label(f"firstrescale{tag}")
+    for qb in (0, 1):
+        tl, mr = T0 + 1 + qb, MREF + qb
+        em.valu(f"v_cndmask_b32_e64 v{mr}, v{mr}, v{tl}, s[{80 + 2 * qb}:{81 + 2 * qb}]", (mr, tl),
+                (mr,), mask_in=f"s{80 + 2 * qb}")
     em.label(f"norescale{tag}")
 
 

@@ -3,8 +3,8 @@
 The GPU tests hold its results bit-identical to the compiler-scheduled kernel; these re-read the
 emitted text with checkers written independently of the generator's own bookkeeping:
   * every branch target is defined once and every label is reached;
-  * along execution paths through the loop (steady tiles, rescale and mask, a wave's last tile,
-    a wave past its last tile), the wait states the generator promises hold: 20 between an
+  * along execution paths through the loop (steady tiles, rescale and mask, a wave's first
+    finite tile, its last tile, a wave past its last tile), the wait states the generator promises hold: 20 between an
     MFMA writing a register and a VALU touching it, 4 between a VALU write and an MFMA reading
     it, 2 after an exponential or a VCC write, 2 between an MFMA reading a fragment quad and
     the LDS read refilling it, 1 between an M0 write and the DMA (an instruction is one wait
@@ -143,6 +143,8 @@ POLICIES = {
     "rescale and mask": lambda lab, k: ("loop" in lab and k <= 2) or "_busy" in lab
     or "domask" in lab,
     "last tile": lambda lab, k: ("loop" in lab and k <= 2) or "_busy" in lab or "_last" in lab,
+    "first finite tile": lambda lab, k: ("loop" in lab and k <= 2) or "_busy" in lab
+    or "firstrescale" in lab or "domask" in lab,
     "idle wave": lambda lab, k: ("loop" in lab and k <= 2) or "nomask" in lab,
 }
 
