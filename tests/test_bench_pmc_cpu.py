@@ -52,3 +52,15 @@ def test_falls_back_to_the_committed_summary(monkeypatch):
     traffic, info = bench.pmc_traffic(live=True)
     assert info["source"] == "profiles/logsumexp_bf16_16384x32000_pmc.md"
     assert traffic is not None and traffic > 1_048_608_768
+
+
+def test_cfg5_annotation_names_the_selected_kernel_and_its_profile():
+    """The cfg5 entry names the head-dim-128 kernel attention.use_w64 picks at its shape, and
+    its MFMA figures come from that kernel's committed counter summary."""
+    from neptune_codegen import attention as A
+
+    assert bench.kernel_of(True).startswith(
+        "64 queries" if A.use_w64(128, True, 4096, 4096) else "32 queries")
+    assert bench.kernel_of(False).startswith("64 queries")
+    pmc = bench.attention_pmc()
+    assert pmc is not None and 0.3 < pmc["mfma_busy_frac"] < 0.8 and 1.0 < pmc["clock_ghz_first_call"] < 2.5
